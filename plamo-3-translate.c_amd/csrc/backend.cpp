@@ -1,0 +1,1422 @@
+// MI355X backend of the PLaMo-3-Translate token loop.
+//
+// Implements the reference's GPU backend API (runtime/metal.h:48-88) on HIP:
+// it replaces runtime/metal.m, runtime/metal_model.m and runtime/metal_weights.m.
+// Weights named by the config mappings or by preload() are copied to HBM once.
+// KV caches, rotated keys and workspace live in HBM; the model's host arrays
+// are refreshed before each successful call returns (the reference shares
+// them zero-copy with the GPU, runtime/metal_model.m:57-119), and host edits
+// between calls are detected and uploaded. A decode step is one hipGraph.
+#include "../../include/plamo_backend.h"
+#include "../../include/plamo_compute.h"
+#include "kernels.h"
+
+#include <hip/hip_runtime.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <algorithm>
+#include <chrono>
+#include <vector>
+
+using namespace plamo;
+
+// CPU kernels of the reference platform (runtime/parallel.h:21-22). Used only
+// when a projection hook cannot run on the GPU, as runtime/metal.m:398-409
+// does; absent on platforms without the reference CPU layer.
+extern "C" void plamo_bf16_matvec_serial(const uint16_t *, const float *, float *, uint64_t,
+                                         uint64_t) __attribute__((weak));
+extern "C" void plamo_bf16_matmul_core(const struct plamo_matmul *) __attribute__((weak));
+
+namespace {
+
+constexpr float kAttentionOffset = 0.2f;                  // src/layer.s:51
+constexpr float kMlpOffset = 0.08944271909999159f;        // src/model.s:111
+constexpr uint64_t kInitialRows = 8192;
+constexpr uint32_t kDecodeSplits = 8;
+constexpr uint64_t kMaxPrompt = 4096;                     // runtime/metal_model.m:540
+
+struct Range {
+    uintptr_t host;
+    uint64_t bytes;
+    char *dev;
+};
+
+struct RopeTable {
+    std::vector<float> freq;  // host copy used as the identity of the table
+    uint32_t dim = 0;
+    uint32_t scale_bits = 0;
+    float *freq_dev = nullptr;
+    float *table = nullptr;   // [rows][dim]: cos | sin
+    uint64_t rows = 0;
+};
+
+struct Layer {
+    const uint16_t *qkv = nullptr, *o = nullptr, *gu = nullptr, *down = nullptr;
+    uint16_t *norms = nullptr;  // device: pre | post | mlp_pre | mlp_post | qn | kn
+    const uint16_t *pre, *post, *mlp_pre, *mlp_post, *qn, *kn;
+    uint32_t qh = 0, kh = 0, dim = 0, hidden = 0, inter = 0, width = 0;
+    uint64_t capacity = 0;
+    bool sliding = false;
+    uint32_t rope = 0;
+    float *k = nullptr, *v = nullptr, *rot = nullptr;
+    uint64_t rows = 0;          // device rows allocated
+    // Shadow of the host bookkeeping after this backend's last return.
+    bool synced = false;
+    uint64_t count = 0, processed = 0, scale_bits = 0;
+    std::vector<float> last_k;
+    uint64_t verify_prefix = 0;
+    bool verify_stale = false;  // device rebuilt rotated rows the host still has stale
+};
+
+struct Buffer {
+    void *ptr = nullptr;
+    size_t bytes = 0;
+};
+
+}  // namespace
+
+struct plamo_metal {
+    plamo_metal_config config{};
+    plamo_metal_info info{};
+    int device = 0;
+    int cus = 256;
+    hipStream_t stream = nullptr;
+    hipEvent_t start = nullptr, stop = nullptr;
+    std::vector<Range> ranges;
+    bool hooks = false;
+
+    struct model *model = nullptr;
+    std::vector<Layer> layers;
+    std::vector<RopeTable> ropes;
+    const uint16_t *embedding = nullptr, *head = nullptr;
+    uint16_t *final_norm = nullptr;
+    uint64_t max_width = 0, max_qkv = 0, max_attention = 0, max_inter = 0, max_cols = 0;
+    uint64_t max_partial = 0;  // qh * (dim + 2) over layers
+
+    StepParams *params_host = nullptr, *params_dev = nullptr;
+    // Decode workspace.
+    float *state_a = nullptr, *state_b = nullptr, *qkv = nullptr, *q = nullptr, *attn = nullptr,
+          *branch = nullptr, *act = nullptr, *down_out = nullptr, *partial = nullptr;
+    uint32_t *counters = nullptr;
+    float *outbox = nullptr, *outbox_host = nullptr;  // logits | state | normalized | stage
+    uint64_t outbox_floats = 0;
+    // Prompt / candidate workspace (grown on demand).
+    uint64_t prompt_rows = 0;
+    Buffer p_state, p_norm, p_qkv, p_q, p_attn, p_branch, p_gu, p_act, p_side_k, p_side_v,
+        p_ids, p_window, p_logits;
+    uint32_t *ids_host = nullptr;
+    // Candidate results kept for commit.
+    float *v_state = nullptr, *v_norm = nullptr, *v_logits = nullptr, *v_prop = nullptr;
+    float *v_host = nullptr;  // pinned: states | normalized | logits | proposals
+    uint32_t *v_next = nullptr, *v_next_host = nullptr;
+    CopyRow *copy_table = nullptr, *copy_table_host = nullptr;
+    uint64_t verification_tokens = 0, verification_index = 0;
+
+    Buffer lin_in, lin_out, mlp_state, mlp_norm, mlp_gu, mlp_act, mlp_branch, mlp_norms;
+
+    hipGraphExec_t graph = nullptr;
+    uint64_t epoch = 1, graph_epoch = 0;
+    std::vector<void *> allocations;
+};
+
+namespace {
+
+int problem(plamo_metal *m, const char *format, ...) {
+    va_list args;
+    va_start(args, format);
+    vsnprintf(m->info.note, sizeof m->info.note, format, args);
+    va_end(args);
+    ++m->info.errors;
+    return 0;
+}
+
+// A failure after device work started: the device KV may no longer match the
+// host arrays, so every layer is uploaded again at the next call. The
+// reference's contract for this case is -1, never retried (runtime/metal.h:63-67).
+int fail(plamo_metal *m) {
+    for (Layer &l : m->layers) l.synced = false;
+    if (m->stream) (void)hipStreamSynchronize(m->stream);
+    (void)hipGetLastError();
+    return -1;
+}
+
+#define HIP_FAIL(m, call)                                                                          \
+    do {                                                                                           \
+        hipError_t e_ = (call);                                                                    \
+        if (e_ != hipSuccess) {                                                                    \
+            problem(m, "%s: %s", #call, hipGetErrorString(e_));                                    \
+            return fail(m);                                                                        \
+        }                                                                                          \
+    } while (0)
+
+#define HIP_TRY(m, call)                                                                           \
+    do {                                                                                           \
+        hipError_t e_ = (call);                                                                    \
+        if (e_ != hipSuccess)                                                                      \
+            return problem(m, "%s: %s", #call, hipGetErrorString(e_));                             \
+    } while (0)
+
+template <typename T>
+T *dev_alloc(plamo_metal *m, uint64_t count) {
+    void *p = nullptr;
+    uint64_t bytes = count * sizeof(T);
+    if (!bytes) bytes = 16;
+    if (hipMalloc(&p, bytes) != hipSuccess) {
+        (void)hipGetLastError();
+        problem(m, "cannot allocate %llu bytes of HBM", (unsigned long long)bytes);
+        return nullptr;
+    }
+    m->allocations.push_back(p);
+    m->info.allocated_bytes += bytes;
+    return (T *)p;
+}
+
+void dev_free(plamo_metal *m, void *p) {
+    if (!p) return;
+    auto it = std::find(m->allocations.begin(), m->allocations.end(), p);
+    if (it != m->allocations.end()) m->allocations.erase(it);
+    (void)hipFree(p);
+}
+
+bool ensure(plamo_metal *m, Buffer &b, uint64_t bytes) {
+    if (b.bytes >= bytes) return true;
+    dev_free(m, b.ptr);
+    b.ptr = dev_alloc<char>(m, bytes);
+    b.bytes = b.ptr ? bytes : 0;
+    return b.ptr != nullptr;
+}
+
+template <typename T>
+T *as(Buffer &b) {
+    return (T *)b.ptr;
+}
+
+uint32_t float_bits(float f) {
+    uint32_t u;
+    memcpy(&u, &f, 4);
+    return u;
+}
+
+// ---------------------------------------------------------------- weights
+const void *resolve(const plamo_metal *m, const void *host, uint64_t bytes) {
+    // Ranges are sorted by start and may nest (a preloaded window inside a
+    // mapping); any range that holds [host, host + bytes) will do.
+    uintptr_t a = (uintptr_t)host;
+    auto it = std::upper_bound(m->ranges.begin(), m->ranges.end(), a,
+                               [](uintptr_t v, const Range &r) { return v < r.host; });
+    while (it != m->ranges.begin()) {
+        --it;
+        if (a + bytes <= it->host + it->bytes) return it->dev + (a - it->host);
+    }
+    return nullptr;
+}
+
+int add_range(plamo_metal *m, const void *host, uint64_t bytes) {
+    if (!host || !bytes) return 1;
+    if (resolve(m, host, bytes)) return 1;
+    char *dev = dev_alloc<char>(m, bytes);
+    if (!dev) return 0;
+    if (hipMemcpy(dev, host, bytes, hipMemcpyHostToDevice) != hipSuccess) {
+        (void)hipGetLastError();
+        dev_free(m, dev);
+        return problem(m, "cannot copy %llu weight bytes to HBM", (unsigned long long)bytes);
+    }
+    Range r{(uintptr_t)host, bytes, dev};
+    m->ranges.insert(std::upper_bound(m->ranges.begin(), m->ranges.end(), r,
+                                      [](const Range &x, const Range &y) { return x.host < y.host; }),
+                     r);
+    m->info.cache.cached_bytes += bytes;
+    m->info.private_weight_bytes += bytes;
+    ++m->info.cache.misses;
+    return 1;
+}
+
+// ---------------------------------------------------------------- model setup
+void release_model(plamo_metal *m) {
+    if (m->graph) {
+        (void)hipGraphExecDestroy(m->graph);
+        m->graph = nullptr;
+    }
+    for (Layer &l : m->layers) {
+        dev_free(m, l.norms);
+        dev_free(m, l.k);
+        dev_free(m, l.v);
+        dev_free(m, l.rot);
+    }
+    for (RopeTable &r : m->ropes) {
+        dev_free(m, r.freq_dev);
+        dev_free(m, r.table);
+    }
+    m->layers.clear();
+    m->ropes.clear();
+    dev_free(m, m->final_norm);
+    m->final_norm = nullptr;
+    m->model = nullptr;
+    m->head = m->embedding = nullptr;
+    m->prompt_rows = 0;
+    for (float **p : {&m->v_state, &m->v_norm, &m->v_logits, &m->v_prop}) {
+        dev_free(m, *p);
+        *p = nullptr;
+    }
+    dev_free(m, m->v_next);
+    m->v_next = nullptr;
+    dev_free(m, m->copy_table);
+    m->copy_table = nullptr;
+    if (m->v_host) (void)hipHostFree(m->v_host);
+    if (m->v_next_host) (void)hipHostFree(m->v_next_host);
+    if (m->copy_table_host) (void)hipHostFree(m->copy_table_host);
+    m->v_host = nullptr;
+    m->v_next_host = nullptr;
+    m->copy_table_host = nullptr;
+    m->verification_tokens = 0;
+    ++m->epoch;
+}
+
+int ensure_rope_rows(plamo_metal *m, RopeTable &r, uint64_t rows) {
+    if (rows <= r.rows) return 1;
+    uint64_t target = r.rows ? r.rows : 128;
+    while (target < rows) target *= 2;
+    float *table = dev_alloc<float>(m, target * r.dim);
+    if (!table) return 0;
+    if (r.rows)
+        HIP_TRY(m, hipMemcpyAsync(table, r.table, r.rows * r.dim * 4, hipMemcpyDeviceToDevice,
+                                  m->stream));
+    float scale;
+    memcpy(&scale, &r.scale_bits, 4);
+    HIP_TRY(m, launch_rope_table(m->stream, r.freq_dev, scale, r.dim / 2, r.rows, target - r.rows,
+                                 table));
+    HIP_TRY(m, hipStreamSynchronize(m->stream));
+    dev_free(m, r.table);
+    r.table = table;
+    r.rows = target;
+    ++m->epoch;
+    return 1;
+}
+
+int ensure_kv_rows(plamo_metal *m, Layer &l, uint64_t rows) {
+    if (rows <= l.rows) return 1;
+    uint64_t target = l.rows ? l.rows : kInitialRows;
+    while (target < rows) target *= 2;
+    if (target > l.capacity) target = l.capacity;
+    float *k = dev_alloc<float>(m, target * l.width), *v = dev_alloc<float>(m, target * l.width),
+          *rot = dev_alloc<float>(m, target * l.width);
+    if (!k || !v || !rot) return 0;
+    if (l.rows) {
+        uint64_t bytes = l.rows * l.width * 4;
+        HIP_TRY(m, hipMemcpyAsync(k, l.k, bytes, hipMemcpyDeviceToDevice, m->stream));
+        HIP_TRY(m, hipMemcpyAsync(v, l.v, bytes, hipMemcpyDeviceToDevice, m->stream));
+        HIP_TRY(m, hipMemcpyAsync(rot, l.rot, bytes, hipMemcpyDeviceToDevice, m->stream));
+        HIP_TRY(m, hipStreamSynchronize(m->stream));
+    }
+    dev_free(m, l.k);
+    dev_free(m, l.v);
+    dev_free(m, l.rot);
+    l.k = k;
+    l.v = v;
+    l.rot = rot;
+    l.rows = target;
+    ++m->epoch;
+    return 1;
+}
+
+int prepare(plamo_metal *m, struct model *model) {
+    if (m->model == model) return 1;
+    release_model(m);
+    if (!model || !model->count || model->count > kMaxLayers || !model->hidden ||
+        model->hidden > UINT32_MAX || !model->vocab || model->vocab > UINT32_MAX ||
+        !model->embedding || !model->head || !model->norm || !model->state ||
+        !model->normalized || !model->logits || !model->scales)
+        return 0;
+    uint64_t h = model->hidden;
+    m->layers.resize(model->count);
+    m->max_width = m->max_qkv = m->max_attention = m->max_inter = m->max_partial = 0;
+    m->max_cols = h;
+    for (uint64_t i = 0; i < model->count; ++i) {
+        const struct layer *l = model->layers[i];
+        const struct qkv *q = l->mixer->qkv;
+        const struct cache *c = l->mixer->cache;
+        const struct rotation *r = l->mixer->rotation;
+        const struct mlp *p = l->mlp;
+        // runtime/metal_model.m:223-235, plus this backend's kernel limits
+        // (head_dim <= 256, at most 8 query heads per KV head).
+        if (l->hidden != h || q->hidden != h || p->hidden != h || l->mixer->hidden != h ||
+            !q->kh || !q->qh || q->qh % q->kh || q->qh / q->kh > 8 || !q->dim || q->dim % 2 ||
+            q->dim > 256 || !c->capacity || c->capacity > UINT32_MAX ||
+            c->width != q->kh * q->dim || r->cache != c || r->heads != q->kh ||
+            r->dim != q->dim || !p->intermediate || p->intermediate > UINT32_MAX / 2 ||
+            !r->freq || !c->k || !c->v || !r->out) {
+            release_model(m);
+            return 0;
+        }
+        Layer &d = m->layers[i];
+        d.qh = (uint32_t)q->qh;
+        d.kh = (uint32_t)q->kh;
+        d.dim = (uint32_t)q->dim;
+        d.hidden = (uint32_t)h;
+        d.inter = (uint32_t)p->intermediate;
+        d.width = (uint32_t)c->width;
+        d.capacity = c->capacity;
+        d.sliding = c->sliding != 0;
+        d.pre = l->pre;
+        d.post = l->post;
+        d.mlp_pre = p->pre;
+        d.mlp_post = p->post;
+        d.qn = q->qn;
+        d.kn = q->kn;
+        // Norm weights are small: always private device copies
+        // (runtime/metal_model.m:294-303 copies them as well).
+        uint64_t words = 4 * h + 2 * (uint64_t)d.dim;
+        d.norms = dev_alloc<uint16_t>(m, words);
+        if (!d.norms) {
+            release_model(m);
+            return 0;
+        }
+        const uint16_t *src[6] = {l->pre, l->post, p->pre, p->post, q->qn, q->kn};
+        uint64_t len[6] = {h, h, h, h, d.dim, d.dim}, off = 0;
+        for (int j = 0; j < 6; ++j) {
+            if (hipMemcpy(d.norms + off, src[j], len[j] * 2, hipMemcpyHostToDevice) != hipSuccess) {
+                (void)hipGetLastError();
+                release_model(m);
+                return problem(m, "cannot copy norm weights");
+            }
+            off += len[j];
+        }
+        uint32_t scale = float_bits(model->scales[i]);
+        size_t rope = 0;
+        for (; rope < m->ropes.size(); ++rope) {
+            RopeTable &t = m->ropes[rope];
+            if (t.dim == d.dim && t.scale_bits == scale &&
+                !memcmp(t.freq.data(), r->freq, d.dim / 2 * sizeof(float)))
+                break;
+        }
+        if (rope == m->ropes.size()) {
+            RopeTable t;
+            t.freq.assign(r->freq, r->freq + d.dim / 2);
+            t.dim = d.dim;
+            t.scale_bits = scale;
+            t.freq_dev = dev_alloc<float>(m, d.dim / 2);
+            if (!t.freq_dev ||
+                hipMemcpy(t.freq_dev, r->freq, d.dim / 2 * 4, hipMemcpyHostToDevice) != hipSuccess) {
+                (void)hipGetLastError();
+                release_model(m);
+                return problem(m, "cannot copy RoPE frequencies");
+            }
+            m->ropes.push_back(std::move(t));
+        }
+        d.rope = (uint32_t)rope;
+        uint64_t want = std::min<uint64_t>(c->capacity, kInitialRows);
+        if (!ensure_rope_rows(m, m->ropes[rope], want) || !ensure_kv_rows(m, d, want)) {
+            release_model(m);
+            return 0;
+        }
+        d.synced = false;
+        d.last_k.assign(d.width, 0.0f);
+        m->max_width = std::max<uint64_t>(m->max_width, d.width);
+        m->max_qkv = std::max<uint64_t>(m->max_qkv, (uint64_t)(d.qh + 2 * d.kh) * d.dim);
+        m->max_attention = std::max<uint64_t>(m->max_attention, (uint64_t)d.qh * d.dim);
+        m->max_inter = std::max<uint64_t>(m->max_inter, d.inter);
+        m->max_partial = std::max<uint64_t>(m->max_partial, (uint64_t)d.qh * (d.dim + 2));
+        m->max_cols = std::max<uint64_t>(m->max_cols, std::max<uint64_t>(d.inter, (uint64_t)d.qh * d.dim));
+    }
+    // The embedding is read one row per token on the device: keep the table
+    // resident even when the engine did not preload it (runtime/engine.c:293-296
+    // skips it on purpose for Apple's shared memory).
+    if (!add_range(m, model->embedding, model->vocab * h * 2)) {
+        release_model(m);
+        return 0;
+    }
+    m->embedding = (const uint16_t *)resolve(m, model->embedding, model->vocab * h * 2);
+    m->final_norm = dev_alloc<uint16_t>(m, h);
+    if (!m->final_norm ||
+        hipMemcpy(m->final_norm, model->norm, h * 2, hipMemcpyHostToDevice) != hipSuccess) {
+        (void)hipGetLastError();
+        release_model(m);
+        return problem(m, "cannot copy the final norm");
+    }
+    if (configure_gemv(m->max_cols) != hipSuccess) {
+        (void)hipGetLastError();
+        release_model(m);
+        return problem(m, "projection width %llu exceeds the LDS budget",
+                       (unsigned long long)m->max_cols);
+    }
+    // Decode workspace.
+    uint64_t L = model->count, V = model->vocab;
+    dev_free(m, m->state_a);
+    dev_free(m, m->state_b);
+    dev_free(m, m->qkv);
+    dev_free(m, m->q);
+    dev_free(m, m->attn);
+    dev_free(m, m->branch);
+    dev_free(m, m->act);
+    dev_free(m, m->down_out);
+    dev_free(m, m->partial);
+    dev_free(m, m->counters);
+    dev_free(m, m->outbox);
+    if (m->outbox_host) (void)hipHostFree(m->outbox_host);
+    m->outbox_host = nullptr;
+    m->state_a = dev_alloc<float>(m, h);
+    m->state_b = dev_alloc<float>(m, h);
+    m->qkv = dev_alloc<float>(m, m->max_qkv);
+    m->q = dev_alloc<float>(m, m->max_attention);
+    m->attn = dev_alloc<float>(m, m->max_attention);
+    m->branch = dev_alloc<float>(m, h);
+    m->act = dev_alloc<float>(m, m->max_inter);
+    m->down_out = dev_alloc<float>(m, h);
+    m->partial = dev_alloc<float>(m, m->max_partial * kDecodeSplits * 4);
+    m->counters = dev_alloc<uint32_t>(m, 256);
+    m->outbox_floats = V + 2 * h + L * 3 * m->max_width;
+    m->outbox = dev_alloc<float>(m, m->outbox_floats);
+    if (!m->state_a || !m->state_b || !m->qkv || !m->q || !m->attn || !m->branch || !m->act ||
+        !m->down_out || !m->partial || !m->counters || !m->outbox ||
+        hipHostMalloc((void **)&m->outbox_host, m->outbox_floats * 4, hipHostMallocDefault) !=
+            hipSuccess ||
+        hipMemset(m->counters, 0, 256 * 4) != hipSuccess) {
+        (void)hipGetLastError();
+        release_model(m);
+        return problem(m, "cannot allocate decode workspace");
+    }
+    m->model = model;
+    ++m->epoch;
+    return 1;
+}
+
+// Projections must already be resident (preloaded or mapped); a miss declines.
+bool resolve_layers(plamo_metal *m, struct model *model) {
+    uint64_t h = model->hidden;
+    for (uint64_t i = 0; i < model->count; ++i) {
+        Layer &d = m->layers[i];
+        if (d.qkv && d.o && d.gu && d.down) continue;
+        const struct layer *l = model->layers[i];
+        const struct qkv *q = l->mixer->qkv;
+        d.qkv = (const uint16_t *)resolve(m, q->weight, (uint64_t)(d.qh + 2 * d.kh) * d.dim * h * 2);
+        d.o = (const uint16_t *)resolve(m, l->mixer->weight, h * d.qh * d.dim * 2);
+        d.gu = (const uint16_t *)resolve(m, l->mlp->gu, 2 * (uint64_t)d.inter * h * 2);
+        d.down = (const uint16_t *)resolve(m, l->mlp->down, (uint64_t)d.inter * h * 2);
+        if (!d.qkv || !d.o || !d.gu || !d.down) {
+            d.qkv = d.o = d.gu = d.down = nullptr;
+            return false;
+        }
+    }
+    if (!m->head) m->head = (const uint16_t *)resolve(m, model->head, model->vocab * h * 2);
+    return m->head != nullptr;
+}
+
+// ---------------------------------------------------------------- host <-> device KV
+// Detects host-side KV edits since this backend's last return (prompt-prefix
+// restore, draft restore, request reset, a CPU step) and uploads the host rows.
+// Sets stale[i] when the device rotated rows must be rebuilt.
+int sync_from_host(plamo_metal *m, struct model *model, std::vector<char> &stale) {
+    stale.assign(model->count, 0);
+    for (uint64_t i = 0; i < model->count; ++i) {
+        Layer &d = m->layers[i];
+        const struct mixer *mx = model->layers[i]->mixer;
+        const struct cache *c = mx->cache;
+        const struct rotation *r = mx->rotation;
+        uint32_t scale = float_bits(model->scales[i]);
+        bool same = d.synced && d.count == c->count && d.processed == r->processed_count &&
+                    d.scale_bits == r->scale_bits &&
+                    (!c->count || !memcmp(c->k + (c->count - 1) * c->width, d.last_k.data(),
+                                          c->width * 4));
+        if (same) {
+            stale[i] = r->processed_count != c->count || r->scale_bits != scale;
+            continue;
+        }
+        if (!ensure_kv_rows(m, d, c->count)) return 0;
+        uint64_t bytes = c->count * c->width * 4;
+        if (bytes) {
+            HIP_TRY(m, hipMemcpyAsync(d.k, c->k, bytes, hipMemcpyHostToDevice, m->stream));
+            HIP_TRY(m, hipMemcpyAsync(d.v, c->v, bytes, hipMemcpyHostToDevice, m->stream));
+        }
+        bool rotated = r->processed_count == c->count && r->scale_bits == scale;
+        if (rotated && bytes)
+            HIP_TRY(m, hipMemcpyAsync(d.rot, r->out, bytes, hipMemcpyHostToDevice, m->stream));
+        stale[i] = !rotated && c->count;
+        d.synced = false;
+    }
+    return 1;
+}
+
+void remember(plamo_metal *m, struct model *model) {
+    for (uint64_t i = 0; i < model->count; ++i) {
+        Layer &d = m->layers[i];
+        const struct mixer *mx = model->layers[i]->mixer;
+        const struct cache *c = mx->cache;
+        d.count = c->count;
+        d.processed = mx->rotation->processed_count;
+        d.scale_bits = mx->rotation->scale_bits;
+        if (c->count) memcpy(d.last_k.data(), c->k + (c->count - 1) * c->width, c->width * 4);
+        d.synced = true;
+    }
+}
+
+void begin_timing(plamo_metal *m) { (void)hipEventRecord(m->start, m->stream); }
+int end_timing(plamo_metal *m) {
+    HIP_TRY(m, hipEventRecord(m->stop, m->stream));
+    HIP_TRY(m, hipEventSynchronize(m->stop));
+    float ms = 0;
+    if (hipEventElapsedTime(&ms, m->start, m->stop) == hipSuccess) m->info.gpu_seconds += ms * 1e-3;
+    ++m->info.command_buffers;
+    return 1;
+}
+
+// ---------------------------------------------------------------- decode
+struct DecodePlan {
+    std::vector<char> stale, shift;
+    bool special = false;
+};
+
+// Enqueues one decode step: embedding, every layer, final norm + head, and the
+// copy of logits/state/normalized/new KV rows to the pinned outbox.
+int encode_decode(plamo_metal *m, struct model *model, const DecodePlan &plan, int *dispatches) {
+    const uint64_t h = model->hidden, V = model->vocab, L = model->count;
+    hipStream_t s = m->stream;
+    int n = 0;
+    float *logits = m->outbox, *state_out = m->outbox + V, *norm_out = m->outbox + V + h;
+    float *stage = m->outbox + V + 2 * h;
+    HIP_TRY(m, hipMemcpyAsync(m->params_dev, m->params_host, sizeof(StepParams),
+                              hipMemcpyHostToDevice, s));
+    HIP_TRY(m, launch_embed(s, m->embedding, nullptr, m->params_dev, 1, (uint32_t)h, m->state_a));
+    ++n;
+    float *cur = m->state_a, *nxt = m->state_b;
+    const int blocks = 2 * m->cus;
+    for (uint64_t i = 0; i < L; ++i) {
+        Layer &d = m->layers[i];
+        const uint16_t *pre = d.norms, *post = d.norms + h, *mpre = d.norms + 2 * h,
+                       *mpost = d.norms + 3 * h, *qn = d.norms + 4 * h, *kn = qn + d.dim;
+        const RopeTable &rope = m->ropes[d.rope];
+        Prologue p1{};
+        p1.src = cur;
+        p1.w = pre;
+        p1.offset = 1.0f;
+        if (i) {
+            p1.branch = m->down_out;
+            p1.rw = m->layers[i - 1].norms + 3 * h;
+            p1.roffset = kMlpOffset;
+            p1.state_out = nxt;
+        }
+        uint64_t qkv_rows = (uint64_t)(d.qh + 2 * d.kh) * d.dim;
+        HIP_TRY(m, launch_gemv(s, d.qkv, qkv_rows, h, p1, m->qkv, 0, blocks));
+        ++n;
+        if (i) std::swap(cur, nxt);
+        const bool shift = plan.shift[i], stale = plan.stale[i];
+        if (stale && !shift) {
+            uint32_t rows = m->params_host->count[i];
+            HIP_TRY(m, launch_rerotate(s, d.k, d.rot, rope.table, rows, d.kh, d.dim));
+            ++n;
+        }
+        QkvPost qp{};
+        qp.qkv = m->qkv;
+        qp.q_out = m->q;
+        qp.qn = qn;
+        qp.kn = kn;
+        qp.table = rope.table;
+        qp.params = m->params_dev;
+        qp.layer = (uint32_t)i;
+        qp.qh = d.qh;
+        qp.kh = d.kh;
+        qp.dim = d.dim;
+        qp.tokens = 1;
+        qp.capacity = (uint32_t)d.capacity;
+        qp.stage = stage + i * 3 * m->max_width;
+        if (shift) {
+            qp.k_raw = as<float>(m->p_side_k);
+            qp.v = as<float>(m->p_side_v);
+            qp.k_rot = nullptr;
+            qp.rows_from_count = 0;
+            qp.rotate_k = 0;
+        } else {
+            qp.k_raw = d.k;
+            qp.v = d.v;
+            qp.k_rot = d.rot;
+            qp.rows_from_count = 1;
+            qp.rotate_k = 1;
+        }
+        HIP_TRY(m, launch_qkv_post(s, qp));
+        ++n;
+        if (shift) {
+            PromptAttention pa{};
+            pa.q = m->q;
+            pa.k_cache = d.k;
+            pa.v_cache = d.v;
+            pa.k_new = as<float>(m->p_side_k);
+            pa.v_new = as<float>(m->p_side_v);
+            pa.table = rope.table;
+            pa.out = m->attn;
+            pa.prefix = (uint32_t)d.capacity;
+            pa.tokens = 1;
+            pa.qh = d.qh;
+            pa.kh = d.kh;
+            pa.dim = d.dim;
+            pa.window = (uint32_t)d.capacity;
+            HIP_TRY(m, launch_prompt_attention(s, pa));
+            HIP_TRY(m, launch_window_store(s, d.k, d.v, d.rot, as<float>(m->p_side_k),
+                                           as<float>(m->p_side_v), d.width, rope.table,
+                                           as<float>(m->p_window), d.capacity, 1, d.capacity,
+                                           d.kh, d.dim));
+            n += 3;
+        } else {
+            DecodeAttention da{};
+            da.q = m->q;
+            da.k_rot = d.rot;
+            da.v = d.v;
+            da.out = m->attn;
+            da.partial = m->partial;
+            da.counters = m->counters;
+            da.params = m->params_dev;
+            da.layer = (uint32_t)i;
+            da.qh = d.qh;
+            da.kh = d.kh;
+            da.dim = d.dim;
+            da.splits = kDecodeSplits;
+            HIP_TRY(m, launch_decode_attention(s, da));
+            ++n;
+        }
+        Prologue po{};
+        po.src = m->attn;
+        HIP_TRY(m, launch_gemv(s, d.o, h, (uint64_t)d.qh * d.dim, po, m->branch, 0, blocks));
+        Prologue pg{};
+        pg.src = cur;
+        pg.w = mpre;
+        pg.offset = 1.0f;
+        pg.branch = m->branch;
+        pg.rw = post;
+        pg.roffset = kAttentionOffset;
+        pg.state_out = nxt;
+        HIP_TRY(m, launch_gemv(s, d.gu, 2 * (uint64_t)d.inter, h, pg, m->act, d.inter, blocks));
+        std::swap(cur, nxt);
+        Prologue pd{};
+        pd.src = m->act;
+        HIP_TRY(m, launch_gemv(s, d.down, h, d.inter, pd, m->down_out, 0, blocks));
+        n += 3;
+        (void)mpost;
+    }
+    Prologue ph{};
+    ph.src = cur;
+    ph.w = m->final_norm;
+    ph.offset = 1.0f;
+    ph.branch = m->down_out;
+    ph.rw = m->layers[L - 1].norms + 3 * h;
+    ph.roffset = kMlpOffset;
+    ph.state_out = state_out;
+    ph.norm_out = norm_out;
+    HIP_TRY(m, launch_gemv(s, m->head, V, h, ph, logits, 0, blocks));
+    ++n;
+    HIP_TRY(m, hipMemcpyAsync(m->outbox_host, m->outbox, m->outbox_floats * 4,
+                              hipMemcpyDeviceToHost, s));
+    *dispatches = n;
+    return 1;
+}
+
+int ensure_prompt(plamo_metal *m, struct model *model, uint64_t rows) {
+    if (rows <= m->prompt_rows && m->p_state.ptr) return 1;
+    uint64_t r = std::max<uint64_t>(rows, 16);
+    uint64_t h = model->hidden;
+    bool ok = ensure(m, m->p_state, r * h * 4) && ensure(m, m->p_norm, r * h * 4) &&
+              ensure(m, m->p_qkv, r * m->max_qkv * 4) && ensure(m, m->p_q, r * m->max_attention * 4) &&
+              ensure(m, m->p_attn, r * m->max_attention * 4) && ensure(m, m->p_branch, r * h * 4) &&
+              ensure(m, m->p_gu, r * 2 * m->max_inter * 4) && ensure(m, m->p_act, r * m->max_inter * 4) &&
+              ensure(m, m->p_side_k, r * m->max_width * 4) &&
+              ensure(m, m->p_side_v, r * m->max_width * 4) && ensure(m, m->p_ids, r * 4);
+    if (!ok) return 0;
+    if (m->ids_host) (void)hipHostFree(m->ids_host);
+    m->ids_host = nullptr;
+    if (hipHostMalloc((void **)&m->ids_host, r * 4, hipHostMallocDefault) != hipSuccess) {
+        (void)hipGetLastError();
+        return problem(m, "cannot allocate pinned id staging");
+    }
+    m->prompt_rows = r;
+    return 1;
+}
+
+int ensure_window_scratch(plamo_metal *m, struct model *model) {
+    uint64_t need = 0;
+    for (uint64_t i = 0; i < model->count; ++i)
+        if (m->layers[i].sliding)
+            need = std::max<uint64_t>(need, 2 * m->layers[i].capacity * m->layers[i].width * 4);
+    return !need || ensure(m, m->p_window, need);
+}
+
+}  // namespace
+
+// ================================================================ public API
+extern "C" {
+
+static int forward_hook(struct model *model, uint64_t token, void *context) {
+    return plamo_metal_forward((struct plamo_metal *)context, model, token);
+}
+static int prefill_hook(struct model *model, const uint32_t *ids, uint64_t n, float *states,
+                        void *context) {
+    return plamo_metal_prefill((struct plamo_metal *)context, model, ids, n, states);
+}
+static int mlp_hook(const struct mlp *mlp, float *states, uint64_t tokens, void *context) {
+    return plamo_metal_mlp((struct plamo_metal *)context, mlp, states, tokens);
+}
+static void matvec_hook(const uint16_t *w, const float *x, float *y, uint64_t rows,
+                        uint64_t cols, void *context) {
+    struct plamo_metal *m = (struct plamo_metal *)context;
+    struct plamo_matmul mm = {w, x, y, rows, cols, 1, cols, rows};
+    if (plamo_metal_linear(m, &mm)) return;
+    ++m->info.cpu_fallbacks;
+    if (plamo_bf16_matvec_serial)
+        plamo_bf16_matvec_serial(w, x, y, rows, cols);
+    else
+        problem(m, "projection not resident and no CPU kernel is linked");
+}
+static void matmul_hook(const struct plamo_matmul *mm, void *context) {
+    struct plamo_metal *m = (struct plamo_metal *)context;
+    if (plamo_metal_linear(m, mm)) return;
+    ++m->info.cpu_fallbacks;
+    if (plamo_bf16_matmul_core)
+        plamo_bf16_matmul_core(mm);
+    else
+        problem(m, "projection not resident and no CPU kernel is linked");
+}
+static const void *identity_provider(const void *p, uint64_t, void *) { return p; }
+
+struct plamo_metal *plamo_metal_open(const struct plamo_metal_config *config, char *error,
+                                     size_t cap) {
+    int devices = 0;
+    if (hipGetDeviceCount(&devices) != hipSuccess || devices < 1) {
+        (void)hipGetLastError();
+        if (error && cap) snprintf(error, cap, "HIP requires an available MI355X (gfx950) GPU");
+        return nullptr;
+    }
+    plamo_metal *m = new plamo_metal();
+    if (config) m->config = *config;
+    hipDeviceProp_t prop;
+    if (hipSetDevice(0) != hipSuccess || hipGetDeviceProperties(&prop, 0) != hipSuccess) {
+        (void)hipGetLastError();
+        if (error && cap) snprintf(error, cap, "cannot open HIP device 0");
+        delete m;
+        return nullptr;
+    }
+    if (strncmp(prop.gcnArchName, "gfx950", 6) != 0) {
+        if (error && cap)
+            snprintf(error, cap, "device %s is not gfx950; this backend is built for MI355X",
+                     prop.gcnArchName);
+        delete m;
+        return nullptr;
+    }
+    m->cus = prop.multiProcessorCount;
+    snprintf(m->info.device, sizeof m->info.device, "%s (%s, %d CUs)", prop.name,
+             prop.gcnArchName, prop.multiProcessorCount);
+    snprintf(m->info.precision, sizeof m->info.precision, "fp32");
+    snprintf(m->info.weight_storage, sizeof m->info.weight_storage, "hbm-bf16");
+    m->info.recommended_working_set_bytes = prop.totalGlobalMem;
+    if (hipStreamCreateWithFlags(&m->stream, hipStreamNonBlocking) != hipSuccess ||
+        hipEventCreate(&m->start) != hipSuccess || hipEventCreate(&m->stop) != hipSuccess ||
+        hipHostMalloc((void **)&m->params_host, sizeof(StepParams), hipHostMallocDefault) !=
+            hipSuccess ||
+        hipMalloc((void **)&m->params_dev, sizeof(StepParams)) != hipSuccess) {
+        (void)hipGetLastError();
+        if (error && cap) snprintf(error, cap, "cannot create HIP stream or staging");
+        plamo_metal_close(m);
+        return nullptr;
+    }
+    memset(m->params_host, 0, sizeof(StepParams));
+    if (m->config.memory != PLAMO_METAL_STREAM)
+        for (size_t i = 0; i < m->config.count && m->config.maps; ++i)
+            if (!add_range(m, m->config.maps[i].base, m->config.maps[i].bytes)) {
+                if (error && cap) snprintf(error, cap, "%s", m->info.note);
+                plamo_metal_close(m);
+                return nullptr;
+            }
+    m->info.cache.budget_bytes = m->info.cache.max_budget_bytes = prop.totalGlobalMem;
+    // runtime/metal.m:900-910: one process-owned backend installs the hooks.
+    if (!plamo_compute_context && !plamo_weight_provider) {
+        plamo_compute_context = m;
+        plamo_matvec_kernel = matvec_hook;
+        plamo_matmul_kernel = matmul_hook;
+        plamo_mlp_kernel = mlp_hook;
+        plamo_forward_kernel = forward_hook;
+        plamo_prefill_kernel = prefill_hook;
+        plamo_weight_provider = identity_provider;
+        plamo_weight_context = nullptr;
+        plamo_weight_chunk_bytes = 0;
+        m->hooks = true;
+    }
+    return m;
+}
+
+void plamo_metal_close(struct plamo_metal *m) {
+    if (!m) return;
+    if (m->stream) (void)hipStreamSynchronize(m->stream);
+    // runtime/metal.m:938-948
+    if (m->hooks && plamo_compute_context == m) {
+        plamo_compute_context = nullptr;
+        plamo_matvec_kernel = nullptr;
+        plamo_matmul_kernel = nullptr;
+        plamo_mlp_kernel = nullptr;
+        plamo_forward_kernel = nullptr;
+        plamo_prefill_kernel = nullptr;
+        plamo_weight_provider = nullptr;
+        plamo_weight_chunk_bytes = 0;
+    }
+    release_model(m);
+    for (void *p : m->allocations) (void)hipFree(p);
+    m->allocations.clear();
+    if (m->outbox_host) (void)hipHostFree(m->outbox_host);
+    if (m->ids_host) (void)hipHostFree(m->ids_host);
+    if (m->v_host) (void)hipHostFree(m->v_host);
+    if (m->v_next_host) (void)hipHostFree(m->v_next_host);
+    if (m->copy_table_host) (void)hipHostFree(m->copy_table_host);
+    if (m->params_host) (void)hipHostFree(m->params_host);
+    if (m->params_dev) (void)hipFree(m->params_dev);
+    if (m->start) (void)hipEventDestroy(m->start);
+    if (m->stop) (void)hipEventDestroy(m->stop);
+    if (m->stream) (void)hipStreamDestroy(m->stream);
+    delete m;
+}
+
+void plamo_metal_maintain(struct plamo_metal *m) {
+    if (m && m->stream) (void)hipStreamSynchronize(m->stream);
+}
+
+void plamo_metal_get_info(const struct plamo_metal *m, struct plamo_metal_info *out) {
+    if (out) *out = m->info;
+}
+
+int plamo_metal_preload(struct plamo_metal *m, const void *ptr, uint64_t bytes) {
+    if (m->config.memory == PLAMO_METAL_STREAM) return 1;
+    if (resolve(m, ptr, bytes)) {
+        ++m->info.cache.hits;
+        m->info.cache.hit_bytes += bytes;
+        return 1;
+    }
+    return add_range(m, ptr, bytes);
+}
+
+int plamo_metal_warm_cache(struct plamo_metal *m) {
+    return hipStreamSynchronize(m->stream) == hipSuccess && hipDeviceSynchronize() == hipSuccess;
+}
+
+int plamo_metal_prepare_model(struct plamo_metal *m, struct model *model) {
+    if (m->config.memory == PLAMO_METAL_STREAM) return 1;
+    return prepare(m, model);
+}
+
+int plamo_metal_forward(struct plamo_metal *m, struct model *model, uint64_t token) {
+    m->verification_tokens = 0;
+    for (Layer &l : m->layers) l.verify_stale = false;
+    if (token >= model->vocab) return -1;
+    if (m->config.memory == PLAMO_METAL_STREAM) return 0;
+    if (!prepare(m, model)) return -1;
+    const uint64_t L = model->count, h = model->hidden, V = model->vocab;
+    // Preflight before touching any state (runtime/metal_model.m:396-421).
+    for (uint64_t i = 0; i < L; ++i) {
+        const struct cache *c = model->layers[i]->mixer->cache;
+        if (c->count > c->capacity || (c->count == c->capacity && !c->sliding)) return -1;
+    }
+    if (!resolve_layers(m, model)) return 0;
+    DecodePlan plan;
+    if (!sync_from_host(m, model, plan.stale)) return -1;
+    plan.shift.assign(L, 0);
+    for (uint64_t i = 0; i < L; ++i) {
+        Layer &d = m->layers[i];
+        const struct cache *c = model->layers[i]->mixer->cache;
+        plan.shift[i] = c->count == c->capacity;
+        if (plan.shift[i] || plan.stale[i]) plan.special = true;
+        uint64_t rows = std::min<uint64_t>(c->count + 1, c->capacity);
+        if (!ensure_kv_rows(m, d, rows) || !ensure_rope_rows(m, m->ropes[d.rope], rows)) return -1;
+        m->params_host->count[i] = (uint32_t)c->count;
+    }
+    if (plan.special && (!ensure_prompt(m, model, 1) || !ensure_window_scratch(m, model))) return -1;
+    m->params_host->token = (uint32_t)token;
+    m->params_host->tokens = 1;
+    int dispatches = 0;
+    begin_timing(m);
+    if (plan.special) {
+        if (!encode_decode(m, model, plan, &dispatches)) return fail(m);
+    } else {
+        if (!m->graph || m->graph_epoch != m->epoch) {
+            if (m->graph) (void)hipGraphExecDestroy(m->graph);
+            m->graph = nullptr;
+            hipGraph_t graph = nullptr;
+            int ok = hipStreamBeginCapture(m->stream, hipStreamCaptureModeThreadLocal) == hipSuccess;
+            int encoded = ok && encode_decode(m, model, plan, &dispatches);
+            ok = hipStreamEndCapture(m->stream, &graph) == hipSuccess && encoded && graph;
+            ok = ok && hipGraphInstantiate(&m->graph, graph, nullptr, nullptr, 0) == hipSuccess;
+            if (graph) (void)hipGraphDestroy(graph);
+            if (!ok) {
+                (void)hipGetLastError();
+                m->graph = nullptr;
+                problem(m, "cannot capture the decode graph");
+                return fail(m);
+            }
+            m->graph_epoch = m->epoch;
+        }
+        dispatches = (int)(3 + 6 * L);
+        if (hipGraphLaunch(m->graph, m->stream) != hipSuccess) {
+            (void)hipGetLastError();
+            problem(m, "decode graph launch failed");
+            return fail(m);
+        }
+    }
+    if (!end_timing(m)) return fail(m);
+    m->info.dispatches += dispatches;
+    // Host mirror (runtime/metal_model.m:491-500).
+    const float *out = m->outbox_host;
+    memcpy(model->logits, out, V * 4);
+    memcpy(model->state, out + V, h * 4);
+    memcpy(model->normalized, out + V + h, h * 4);
+    const float *stage = out + V + 2 * h;
+    for (uint64_t i = 0; i < L; ++i) {
+        Layer &d = m->layers[i];
+        struct mixer *mx = model->layers[i]->mixer;
+        struct cache *c = mx->cache;
+        struct rotation *r = mx->rotation;
+        const float *st = stage + i * 3 * m->max_width;
+        uint64_t row = c->count;
+        if (plan.shift[i]) {
+            memmove(c->k, c->k + c->width, (c->capacity - 1) * c->width * 4);
+            memmove(c->v, c->v + c->width, (c->capacity - 1) * c->width * 4);
+            row = c->capacity - 1;
+        }
+        memcpy(c->k + row * c->width, st, c->width * 4);
+        memcpy(c->v + row * c->width, st + c->width, c->width * 4);
+        uint64_t count = row + 1;
+        if (plan.shift[i] || plan.stale[i]) {
+            if (hipMemcpy(r->out, d.rot, count * c->width * 4, hipMemcpyDeviceToHost) != hipSuccess) {
+                problem(m, "cannot mirror rotated keys");
+                return fail(m);
+            }
+        } else {
+            memcpy(r->out + row * c->width, st + 2 * c->width, c->width * 4);
+        }
+        c->count = count;
+        r->processed_count = count;
+        r->scale_bits = float_bits(model->scales[i]);
+    }
+    remember(m, model);
+    ++m->info.fused_decodes;
+    m->info.fused_mlps += L;
+    return 1;
+}
+
+}  // extern "C"
+
+namespace {
+
+// Layer-major prompt processing shared by prefill (verify == false) and
+// candidate verification (verify == true). Returns 1, 0 (declined, nothing
+// changed) or -1.
+int run_prompt(plamo_metal *m, struct model *model, const uint32_t *ids, uint64_t T,
+               float *states, bool verify) {
+    m->verification_tokens = 0;
+    for (Layer &l : m->layers) l.verify_stale = false;
+    if (!model || !ids || !T) return -1;
+    if (m->config.memory == PLAMO_METAL_STREAM || T > kMaxPrompt) return 0;
+    for (uint64_t t = 0; t < T; ++t)
+        if (ids[t] >= model->vocab) return -1;
+    if (!prepare(m, model)) return -1;
+    const uint64_t L = model->count, h = model->hidden, V = model->vocab;
+    for (uint64_t i = 0; i < L; ++i) {
+        const struct cache *c = model->layers[i]->mixer->cache;
+        if (c->count > c->capacity || (!c->sliding && T > c->capacity - c->count)) return -1;
+    }
+    if (!resolve_layers(m, model)) return 0;
+    std::vector<char> stale;
+    if (!sync_from_host(m, model, stale)) return -1;
+    if (!ensure_prompt(m, model, T) || !ensure_window_scratch(m, model)) return -1;
+    if (verify) {
+        uint64_t prop = L * 3 * kMaxVerify * m->max_width;
+        if (!m->v_state) {
+            m->v_state = dev_alloc<float>(m, kMaxVerify * h);
+            m->v_norm = dev_alloc<float>(m, kMaxVerify * h);
+            m->v_logits = dev_alloc<float>(m, kMaxVerify * V);
+            m->v_prop = dev_alloc<float>(m, prop);
+            m->v_next = dev_alloc<uint32_t>(m, kMaxVerify);
+            m->copy_table = dev_alloc<CopyRow>(m, 3 * kMaxLayers);
+            if (!m->v_state || !m->v_norm || !m->v_logits || !m->v_prop || !m->v_next ||
+                !m->copy_table ||
+                hipHostMalloc((void **)&m->v_host, (kMaxVerify * (2 * h + V) + prop) * 4,
+                              hipHostMallocDefault) != hipSuccess ||
+                hipHostMalloc((void **)&m->v_next_host, kMaxVerify * 4, hipHostMallocDefault) !=
+                    hipSuccess ||
+                hipHostMalloc((void **)&m->copy_table_host, 3 * kMaxLayers * sizeof(CopyRow),
+                              hipHostMallocDefault) != hipSuccess) {
+                (void)hipGetLastError();
+                return problem(m, "cannot allocate verification buffers") - 1;
+            }
+        }
+    }
+    std::vector<char> overflow(L, 0);
+    for (uint64_t i = 0; i < L; ++i) {
+        Layer &d = m->layers[i];
+        const struct cache *c = model->layers[i]->mixer->cache;
+        overflow[i] = c->count + T > c->capacity;
+        uint64_t rows = std::min<uint64_t>(c->count + T, c->capacity);
+        if (!ensure_kv_rows(m, d, rows) || !ensure_rope_rows(m, m->ropes[d.rope], rows)) return -1;
+        m->params_host->count[i] = (uint32_t)c->count;
+    }
+    m->params_host->tokens = (uint32_t)T;
+    memcpy(m->ids_host, ids, T * 4);
+    hipStream_t s = m->stream;
+    int n = 0;
+    begin_timing(m);
+    HIP_FAIL(m, hipMemcpyAsync(m->params_dev, m->params_host, sizeof(StepParams),
+                              hipMemcpyHostToDevice, s));
+    HIP_FAIL(m, hipMemcpyAsync(m->p_ids.ptr, m->ids_host, T * 4, hipMemcpyHostToDevice, s));
+    float *state = as<float>(m->p_state), *norm = as<float>(m->p_norm), *qkv = as<float>(m->p_qkv),
+          *q = as<float>(m->p_q), *attn = as<float>(m->p_attn), *branch = as<float>(m->p_branch),
+          *gu = as<float>(m->p_gu), *act = as<float>(m->p_act);
+    HIP_FAIL(m, launch_embed(s, m->embedding, as<uint32_t>(m->p_ids), nullptr, (uint32_t)T,
+                            (uint32_t)h, state));
+    ++n;
+    for (uint64_t i = 0; i < L; ++i) {
+        Layer &d = m->layers[i];
+        const struct cache *c = model->layers[i]->mixer->cache;
+        const uint16_t *pre = d.norms, *post = d.norms + h, *mpre = d.norms + 2 * h,
+                       *mpost = d.norms + 3 * h, *qn = d.norms + 4 * h, *kn = qn + d.dim;
+        const RopeTable &rope = m->ropes[d.rope];
+        const uint64_t qkv_w = (uint64_t)(d.qh + 2 * d.kh) * d.dim, aw = (uint64_t)d.qh * d.dim;
+        HIP_FAIL(m, launch_norm_rows(s, state, h, pre, 1.0f, norm, h, h, T));
+        HIP_FAIL(m, launch_gemm(s, norm, h, d.qkv, qkv_w, h, T, qkv, qkv_w));
+        n += 2;
+        if (stale[i] && (verify || !overflow[i])) {
+            HIP_FAIL(m, launch_rerotate(s, d.k, d.rot, rope.table, c->count, d.kh, d.dim));
+            d.verify_stale = verify;
+            ++n;
+        }
+        float *prop_k = nullptr, *prop_v = nullptr, *prop_r = nullptr;
+        if (verify) {
+            prop_k = m->v_prop + ((i * 3 + 0) * kMaxVerify) * m->max_width;
+            prop_v = m->v_prop + ((i * 3 + 1) * kMaxVerify) * m->max_width;
+            prop_r = m->v_prop + ((i * 3 + 2) * kMaxVerify) * m->max_width;
+        }
+        QkvPost qp{};
+        qp.qkv = qkv;
+        qp.q_out = q;
+        qp.qn = qn;
+        qp.kn = kn;
+        qp.table = rope.table;
+        qp.params = m->params_dev;
+        qp.layer = (uint32_t)i;
+        qp.qh = d.qh;
+        qp.kh = d.kh;
+        qp.dim = d.dim;
+        qp.tokens = (uint32_t)T;
+        qp.capacity = (uint32_t)d.capacity;
+        if (verify) {
+            qp.k_raw = prop_k;
+            qp.v = prop_v;
+            qp.k_rot = prop_r;
+            qp.rows_from_count = 0;
+            qp.rotate_k = 1;
+        } else if (overflow[i]) {
+            qp.k_raw = as<float>(m->p_side_k);
+            qp.v = as<float>(m->p_side_v);
+            qp.rows_from_count = 0;
+            qp.rotate_k = 0;
+        } else {
+            qp.k_raw = d.k;
+            qp.v = d.v;
+            qp.k_rot = d.rot;
+            qp.rows_from_count = 1;
+            qp.rotate_k = 1;
+        }
+        HIP_FAIL(m, launch_qkv_post(s, qp));
+        ++n;
+        PromptAttention pa{};
+        pa.q = q;
+        pa.table = rope.table;
+        pa.out = attn;
+        pa.prefix = (uint32_t)c->count;
+        pa.tokens = (uint32_t)T;
+        pa.qh = d.qh;
+        pa.kh = d.kh;
+        pa.dim = d.dim;
+        if (overflow[i]) {
+            pa.k_cache = d.k;
+            pa.v_cache = d.v;
+            pa.k_new = verify ? prop_k : as<float>(m->p_side_k);
+            pa.v_new = verify ? prop_v : as<float>(m->p_side_v);
+            pa.window = (uint32_t)d.capacity;
+        } else {
+            pa.k_cache = d.rot;
+            pa.v_cache = d.v;
+            pa.k_new = verify ? prop_r : d.rot + c->count * d.width;
+            pa.v_new = verify ? prop_v : d.v + c->count * d.width;
+            pa.window = 0;
+        }
+        HIP_FAIL(m, launch_prompt_attention(s, pa));
+        ++n;
+        if (overflow[i] && !verify) {
+            HIP_FAIL(m, launch_window_store(s, d.k, d.v, d.rot, as<float>(m->p_side_k),
+                                           as<float>(m->p_side_v), d.width, rope.table,
+                                           as<float>(m->p_window), c->count, T, d.capacity, d.kh,
+                                           d.dim));
+            n += 2;
+        }
+        // With states == NULL only the final row feeds the logits; the last
+        // layer's projection and MLP run for that row alone
+        // (runtime/metal_model.m:761-770).
+        uint64_t first = 0, rows = T;
+        if (!verify && !states && i + 1 == L && T > 1) {
+            first = T - 1;
+            rows = 1;
+        }
+        float *st = state + first * h;
+        HIP_FAIL(m, launch_gemm(s, attn + first * aw, aw, d.o, h, aw, rows, branch, h));
+        HIP_FAIL(m, launch_residual_rows(s, st, branch, post, kAttentionOffset, h, rows));
+        HIP_FAIL(m, launch_norm_rows(s, st, h, mpre, 1.0f, norm, h, h, rows));
+        HIP_FAIL(m, launch_gemm(s, norm, h, d.gu, 2 * (uint64_t)d.inter, h, rows, gu,
+                               2 * (uint64_t)d.inter));
+        HIP_FAIL(m, launch_swiglu_rows(s, gu, act, d.inter, rows));
+        HIP_FAIL(m, launch_gemm(s, act, d.inter, d.down, h, d.inter, rows, branch, h));
+        HIP_FAIL(m, launch_residual_rows(s, st, branch, mpost, kMlpOffset, h, rows));
+        n += 7;
+    }
+    if (verify) {
+        HIP_FAIL(m, launch_norm_rows(s, state, h, m->final_norm, 1.0f, m->v_norm, h, h, T));
+        HIP_FAIL(m, launch_gemm(s, m->v_norm, h, m->head, V, h, T, m->v_logits, V));
+        HIP_FAIL(m, launch_argmax_rows(s, m->v_logits, V, T, m->v_next));
+        HIP_FAIL(m, hipMemcpyAsync(m->v_state, state, T * h * 4, hipMemcpyDeviceToDevice, s));
+        HIP_FAIL(m, hipMemcpyAsync(m->v_host, m->v_state, T * h * 4, hipMemcpyDeviceToHost, s));
+        HIP_FAIL(m, hipMemcpyAsync(m->v_host + kMaxVerify * h, m->v_norm, T * h * 4,
+                                  hipMemcpyDeviceToHost, s));
+        HIP_FAIL(m, hipMemcpyAsync(m->v_host + 2 * kMaxVerify * h, m->v_logits, T * V * 4,
+                                  hipMemcpyDeviceToHost, s));
+        HIP_FAIL(m, hipMemcpyAsync(m->v_host + kMaxVerify * (2 * h + V), m->v_prop,
+                                  L * 3 * kMaxVerify * m->max_width * 4, hipMemcpyDeviceToHost, s));
+        HIP_FAIL(m, hipMemcpyAsync(m->v_next_host, m->v_next, T * 4, hipMemcpyDeviceToHost, s));
+        n += 3;
+    } else {
+        const float *last = state + (T - 1) * h;
+        Prologue ph{};
+        ph.src = last;
+        ph.w = m->final_norm;
+        ph.offset = 1.0f;
+        ph.norm_out = m->outbox + V + h;
+        HIP_FAIL(m, launch_gemv(s, m->head, V, h, ph, m->outbox, 0, 2 * m->cus));
+        HIP_FAIL(m, hipMemcpyAsync(m->outbox + V, last, h * 4, hipMemcpyDeviceToDevice, s));
+        HIP_FAIL(m, hipMemcpyAsync(m->outbox_host, m->outbox, (V + 2 * h) * 4,
+                                  hipMemcpyDeviceToHost, s));
+        ++n;
+    }
+    if (!end_timing(m)) return fail(m);
+    m->info.dispatches += n;
+    if (verify) {
+        m->verification_tokens = T;
+        m->verification_index = 0;
+        for (uint64_t i = 0; i < L; ++i) m->layers[i].verify_prefix = model->layers[i]->mixer->cache->count;
+        ++m->info.verification_batches;
+        m->info.verified_tokens += T;
+        return 1;
+    }
+    // Host mirror: prompt states, final state / normalized / logits, new KV rows.
+    if (states && hipMemcpy(states, state, T * h * 4, hipMemcpyDeviceToHost) != hipSuccess) {
+        problem(m, "cannot copy prompt states");
+        return fail(m);
+    }
+    memcpy(model->logits, m->outbox_host, V * 4);
+    memcpy(model->state, m->outbox_host + V, h * 4);
+    memcpy(model->normalized, m->outbox_host + V + h, h * 4);
+    for (uint64_t i = 0; i < L; ++i) {
+        Layer &d = m->layers[i];
+        struct mixer *mx = model->layers[i]->mixer;
+        struct cache *c = mx->cache;
+        struct rotation *r = mx->rotation;
+        uint64_t first = overflow[i] ? 0 : c->count;
+        uint64_t end = std::min<uint64_t>(c->count + T, c->capacity);
+        uint64_t rot_first = (overflow[i] || stale[i]) ? 0 : first;
+        uint64_t w = c->width * 4;
+        if (hipMemcpy(c->k + first * c->width, d.k + first * c->width, (end - first) * w,
+                      hipMemcpyDeviceToHost) != hipSuccess ||
+            hipMemcpy(c->v + first * c->width, d.v + first * c->width, (end - first) * w,
+                      hipMemcpyDeviceToHost) != hipSuccess ||
+            hipMemcpy(r->out + rot_first * c->width, d.rot + rot_first * c->width,
+                      (end - rot_first) * w, hipMemcpyDeviceToHost) != hipSuccess) {
+            problem(m, "cannot mirror prompt KV rows");
+            return fail(m);
+        }
+        c->count = end;
+        r->processed_count = end;
+        r->scale_bits = float_bits(model->scales[i]);
+    }
+    remember(m, model);
+    ++m->info.fused_prefills;
+    m->info.fused_mlps += L;
+    return 1;
+}
+
+}  // namespace
+
+extern "C" {
+
+int plamo_metal_prefill(struct plamo_metal *m, struct model *model, const uint32_t *ids,
+                        uint64_t tokens, float *states) {
+    return run_prompt(m, model, ids, tokens, states, false);
+}
+
+int plamo_metal_verify(struct plamo_metal *m, struct model *model, const uint32_t *ids,
+                       uint64_t tokens, uint32_t *next) {
+    if (!next || !tokens || tokens > PLAMO_VERIFY_MAX) return 0;
+    int result = run_prompt(m, model, ids, tokens, nullptr, true);
+    if (result == 1) memcpy(next, m->v_next_host, tokens * 4);
+    return result;
+}
+
+int plamo_metal_commit(struct plamo_metal *m, struct model *model, uint64_t index) {
+    if (m->model != model || index != m->verification_index || index >= m->verification_tokens)
+        return 0;
+    const uint64_t L = model->count, h = model->hidden, V = model->vocab;
+    bool full = false;
+    for (uint64_t i = 0; i < L; ++i) {
+        const struct cache *c = model->layers[i]->mixer->cache;
+        uint64_t count = std::min<uint64_t>(m->layers[i].verify_prefix + index, c->capacity);
+        if (c->count != count) return 0;
+        if (c->count == c->capacity) {
+            if (!c->sliding) return 0;
+            full = true;
+        }
+    }
+    // Candidate rows were rotated at positions prefix + index; ordinary
+    // appends only copy them (runtime/metal_model.m:881-900). A full sliding
+    // window is rebased on the device instead.
+    const float *prop_host = m->v_host + kMaxVerify * (2 * h + V);
+    uint32_t entries = 0;
+    begin_timing(m);
+    for (uint64_t i = 0; i < L; ++i) {
+        Layer &d = m->layers[i];
+        const struct cache *c = model->layers[i]->mixer->cache;
+        float *pk = m->v_prop + ((i * 3 + 0) * kMaxVerify + index) * m->max_width;
+        float *pv = m->v_prop + ((i * 3 + 1) * kMaxVerify + index) * m->max_width;
+        float *pr = m->v_prop + ((i * 3 + 2) * kMaxVerify + index) * m->max_width;
+        if (c->count < c->capacity) {
+            m->copy_table_host[entries++] = CopyRow{pk, d.k + c->count * d.width, d.width};
+            m->copy_table_host[entries++] = CopyRow{pv, d.v + c->count * d.width, d.width};
+            m->copy_table_host[entries++] = CopyRow{pr, d.rot + c->count * d.width, d.width};
+        } else {
+            HIP_FAIL(m, launch_window_store(m->stream, d.k, d.v, d.rot, pk, pv, d.width,
+                                           m->ropes[d.rope].table, as<float>(m->p_window),
+                                           c->capacity, 1, c->capacity, d.kh, d.dim));
+            m->info.dispatches += 2;
+        }
+    }
+    if (entries) {
+        HIP_FAIL(m, hipMemcpyAsync(m->copy_table, m->copy_table_host, entries * sizeof(CopyRow),
+                                  hipMemcpyHostToDevice, m->stream));
+        HIP_FAIL(m, launch_copy_rows(m->stream, m->copy_table, entries));
+        ++m->info.dispatches;
+    }
+    if (!end_timing(m)) return fail(m);
+    for (uint64_t i = 0; i < L; ++i) {
+        Layer &d = m->layers[i];
+        struct mixer *mx = model->layers[i]->mixer;
+        struct cache *c = mx->cache;
+        struct rotation *r = mx->rotation;
+        const float *hk = prop_host + ((i * 3 + 0) * kMaxVerify + index) * m->max_width;
+        const float *hv = prop_host + ((i * 3 + 1) * kMaxVerify + index) * m->max_width;
+        const float *hr = prop_host + ((i * 3 + 2) * kMaxVerify + index) * m->max_width;
+        if (c->count < c->capacity) {
+            memcpy(c->k + c->count * c->width, hk, c->width * 4);
+            memcpy(c->v + c->count * c->width, hv, c->width * 4);
+            memcpy(r->out + c->count * c->width, hr, c->width * 4);
+            ++c->count;
+        } else {
+            memmove(c->k, c->k + c->width, (c->capacity - 1) * c->width * 4);
+            memmove(c->v, c->v + c->width, (c->capacity - 1) * c->width * 4);
+            memcpy(c->k + (c->capacity - 1) * c->width, hk, c->width * 4);
+            memcpy(c->v + (c->capacity - 1) * c->width, hv, c->width * 4);
+            if (hipMemcpy(r->out, d.rot, c->capacity * c->width * 4, hipMemcpyDeviceToHost) !=
+                hipSuccess) {
+                problem(m, "cannot mirror rotated keys");
+                return fail(m);
+            }
+        }
+        if (d.verify_stale && c->count < c->capacity) {
+            if (hipMemcpy(r->out, d.rot, c->count * c->width * 4, hipMemcpyDeviceToHost) !=
+                hipSuccess) {
+                problem(m, "cannot mirror rotated keys");
+                return fail(m);
+            }
+        }
+        d.verify_stale = false;
+        r->processed_count = c->count;
+        r->scale_bits = float_bits(model->scales[i]);
+    }
+    (void)full;
+    memcpy(model->state, m->v_host + index * h, h * 4);
+    memcpy(model->normalized, m->v_host + kMaxVerify * h + index * h, h * 4);
+    memcpy(model->logits, m->v_host + 2 * kMaxVerify * h + index * V, V * 4);
+    remember(m, model);
+    ++m->verification_index;
+    ++m->info.committed_tokens;
+    return 1;
+}
+
+int plamo_metal_linear(struct plamo_metal *m, const struct plamo_matmul *mm) {
+    if (!mm || !mm->rows || !mm->columns || !mm->tokens || mm->input_stride < mm->columns ||
+        mm->output_stride < mm->rows)
+        return 0;
+    const uint16_t *w =
+        (const uint16_t *)resolve(m, mm->weights, mm->rows * mm->columns * 2);
+    if (!w) return 0;
+    uint64_t T = mm->tokens, K = mm->columns, N = mm->rows;
+    Buffer &in = m->lin_in, &out = m->lin_out;
+    if (!ensure(m, in, T * K * 4) || !ensure(m, out, T * N * 4)) return 0;
+    if (T == 1 && configure_gemv(K) != hipSuccess) {
+        (void)hipGetLastError();
+        return 0;
+    }
+    int ok = hipMemcpy2DAsync(in.ptr, K * 4, mm->input, mm->input_stride * 4, K * 4, T,
+                              hipMemcpyHostToDevice, m->stream) == hipSuccess;
+    begin_timing(m);
+    if (ok && T == 1) {
+        Prologue p{};
+        p.src = as<float>(in);
+        ok = launch_gemv(m->stream, w, N, K, p, as<float>(out), 0, 2 * m->cus) == hipSuccess;
+    } else if (ok) {
+        ok = launch_gemm(m->stream, as<float>(in), K, w, N, K, T, as<float>(out), N) == hipSuccess;
+    }
+    ok = ok && hipMemcpy2DAsync(mm->output, mm->output_stride * 4, out.ptr, N * 4, N * 4, T,
+                                hipMemcpyDeviceToHost, m->stream) == hipSuccess;
+    ok = ok && end_timing(m);
+    if (!ok) {
+        (void)hipGetLastError();
+        return problem(m, "projection failed");
+    }
+    ++m->info.dispatches;
+    return 1;
+}
+
+int plamo_metal_mlp(struct plamo_metal *m, const struct mlp *mlp, float *states, uint64_t tokens) {
+    if (!mlp || !states || !tokens || !mlp->hidden || !mlp->intermediate) return 0;
+    uint64_t h = mlp->hidden, I = mlp->intermediate, T = tokens;
+    const uint16_t *gu = (const uint16_t *)resolve(m, mlp->gu, 2 * I * h * 2);
+    const uint16_t *down = (const uint16_t *)resolve(m, mlp->down, I * h * 2);
+    if (!gu || !down) return 0;
+    if (configure_gemv(std::max<uint64_t>(h, I)) != hipSuccess) {
+        (void)hipGetLastError();
+        return 0;
+    }
+    Buffer &st = m->mlp_state, &nrm = m->mlp_norm, &g = m->mlp_gu, &a = m->mlp_act,
+           &b = m->mlp_branch, &norms = m->mlp_norms;
+    bool ok = ensure(m, st, T * h * 4) && ensure(m, nrm, T * h * 4) && ensure(m, g, T * 2 * I * 4) &&
+              ensure(m, a, T * I * 4) && ensure(m, b, T * h * 4) && ensure(m, norms, 2 * h * 2);
+    hipStream_t s = m->stream;
+    ok = ok && hipMemcpyAsync(norms.ptr, mlp->pre, h * 2, hipMemcpyHostToDevice, s) == hipSuccess &&
+         hipMemcpyAsync(as<uint16_t>(norms) + h, mlp->post, h * 2, hipMemcpyHostToDevice, s) ==
+             hipSuccess &&
+         hipMemcpyAsync(st.ptr, states, T * h * 4, hipMemcpyHostToDevice, s) == hipSuccess;
+    if (ok) begin_timing(m);
+    ok = ok && launch_norm_rows(s, as<float>(st), h, as<uint16_t>(norms), 1.0f, as<float>(nrm), h, h, T) == hipSuccess &&
+         launch_gemm(s, as<float>(nrm), h, gu, 2 * I, h, T, as<float>(g), 2 * I) == hipSuccess &&
+         launch_swiglu_rows(s, as<float>(g), as<float>(a), I, T) == hipSuccess &&
+         launch_gemm(s, as<float>(a), I, down, h, I, T, as<float>(b), h) == hipSuccess &&
+         launch_residual_rows(s, as<float>(st), as<float>(b), as<uint16_t>(norms) + h, kMlpOffset, h, T) == hipSuccess &&
+         hipMemcpyAsync(states, st.ptr, T * h * 4, hipMemcpyDeviceToHost, s) == hipSuccess &&
+         end_timing(m);
+    if (!ok) {
+        (void)hipGetLastError();
+        return problem(m, "MLP failed");
+    }
+    m->info.dispatches += 5;
+    ++m->info.fused_mlps;
+    return 1;
+}
+
+}  // extern "C"

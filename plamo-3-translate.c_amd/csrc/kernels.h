@@ -1,0 +1,122 @@
+// Launchers of the gfx950 token-loop kernels (implemented in kernels.hip).
+//
+// Every launcher enqueues on the given stream and returns the launch status.
+// Shapes are checked by the caller (backend.cpp) before any launch: a kernel
+// trusts its sizes, so a wrong size would fault instead of failing.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace plamo {
+
+// Per-call values the kernels read from device memory, so a captured decode
+// graph stays valid from one step to the next (the host rewrites this block
+// before every launch).
+enum { kMaxLayers = 128, kMaxVerify = 16 };
+struct StepParams {
+    uint32_t token;             // decode token id
+    uint32_t tokens;            // prompt / candidate rows of this call
+    uint32_t count[kMaxLayers]; // cache rows of each layer before this call
+};
+
+// Norm applied in a GEMV prologue: x = rms(src) * (bf16(w) + offset).
+// With residual, the prologue first forms src' = src + rms(branch) *
+// (bf16(rw) + roffset) and block 0 stores src' to state_out.
+struct Prologue {
+    const float *src;        // vector to normalize (or raw input when w == nullptr)
+    const uint16_t *w;       // norm weights; nullptr: use src as is
+    float offset;
+    const float *branch;     // residual branch; nullptr: no residual
+    const uint16_t *rw;
+    float roffset;
+    float *state_out;        // written by block 0 when branch != nullptr
+    float *norm_out;         // written by block 0 when non-null (normalized x)
+};
+
+hipError_t launch_rope_table(hipStream_t, const float *freq, float scale, uint32_t half,
+                             uint64_t first_row, uint64_t rows, float *table);
+hipError_t launch_embed(hipStream_t, const uint16_t *embedding, const uint32_t *ids,
+                        const StepParams *params, uint32_t tokens, uint32_t hidden, float *out);
+// y[r] = W[r,:] . x (x from the prologue). swiglu_half > 0: rows r and
+// r + swiglu_half are gate/up and y[r] = silu(gate) * up for r < swiglu_half.
+hipError_t launch_gemv(hipStream_t, const uint16_t *w, uint64_t rows, uint64_t cols,
+                       const Prologue &pro, float *y, uint64_t swiglu_half, int blocks_hint);
+// C[t, r] = sum_k X[t, k] * W[r, k]; FP32 MFMA, BF16 weights widened in LDS.
+hipError_t launch_gemm(hipStream_t, const float *x, uint64_t x_stride, const uint16_t *w,
+                       uint64_t rows, uint64_t cols, uint64_t tokens, float *y,
+                       uint64_t y_stride);
+// Multi-row RMSNorm; with branch: state += rms(branch) * (bf16(w) + offset).
+hipError_t launch_norm_rows(hipStream_t, const float *x, uint64_t x_stride, const uint16_t *w,
+                            float offset, float *y, uint64_t y_stride, uint64_t width,
+                            uint64_t rows);
+hipError_t launch_residual_rows(hipStream_t, float *state, const float *branch,
+                                const uint16_t *w, float offset, uint64_t width, uint64_t rows);
+hipError_t launch_swiglu_rows(hipStream_t, const float *gate_up, float *out,
+                              uint64_t intermediate, uint64_t rows);
+
+// Q/K head RMSNorm + RoPE + cache append for `tokens` rows of one layer.
+struct QkvPost {
+    float *qkv;              // [tokens, (qh+2kh)*dim] projection output (read)
+    float *q_out;            // [tokens, qh*dim] normalized, rotated Q
+    const uint16_t *qn, *kn;
+    const float *table;      // RoPE rows [position][dim]: cos | sin
+    const StepParams *params;
+    uint32_t layer, qh, kh, dim, tokens, capacity;
+    // K/V destination rows: row t goes to dst_*[(row0 + t) * width], where
+    // row0 = params->count[layer] when rows_from_count, else 0.
+    float *k_raw, *v, *k_rot;
+    int rows_from_count;
+    int rotate_k;            // 0: leave k_rot alone (sliding overflow)
+    float *stage;            // optional [3][width] copy of the last row (decode mirror)
+};
+hipError_t launch_qkv_post(hipStream_t, const QkvPost &);
+
+// Decode attention for one token over rows [0, count+1) of the rotated cache.
+struct DecodeAttention {
+    const float *q;          // [qh*dim]
+    const float *k_rot, *v;  // cache [rows, kh*dim]
+    float *out;              // [qh*dim]
+    float *partial;          // scratch [qh][splits][dim + 2]
+    uint32_t *counters;      // [kh] zero-initialized; reset by the kernel
+    const StepParams *params;
+    uint32_t layer, qh, kh, dim, splits;
+};
+hipError_t launch_decode_attention(hipStream_t, const DecodeAttention &);
+
+// General causal attention for `tokens` query rows. Key j of query t is the
+// virtual row j of [cache rows 0..prefix) ++ [new rows 0..tokens). With
+// window > 0 query t sees only the last `window` virtual rows ending at its
+// own row and keys are rotated on the fly at their window-local position.
+struct PromptAttention {
+    const float *q;          // [tokens, qh*dim] rotated Q
+    const float *k_cache, *v_cache;  // rotated (or raw when window) cache rows
+    const float *k_new, *v_new;      // rotated (or raw when window) new rows
+    const float *table;
+    float *out;              // [tokens, qh*dim]
+    uint32_t prefix, tokens, qh, kh, dim, window;
+};
+hipError_t launch_prompt_attention(hipStream_t, const PromptAttention &);
+
+// Rotates cache rows [0, rows) of raw K into rotated K at their row position.
+hipError_t launch_rerotate(hipStream_t, const float *k_raw, float *k_rot, const float *table,
+                           uint64_t rows, uint32_t kh, uint32_t dim);
+// Sliding-window commit: the final `keep` rows of [cache 0..prefix) ++
+// [new 0..tokens) become cache rows 0..keep, rotated at their new positions.
+hipError_t launch_window_store(hipStream_t, float *k_raw, float *v, float *k_rot,
+                               const float *new_k, const float *new_v, uint64_t new_stride,
+                               const float *table, float *scratch, uint64_t prefix,
+                               uint64_t tokens, uint64_t keep, uint32_t kh, uint32_t dim);
+// Batched row copies (one launch for every layer of a commit).
+struct CopyRow {
+    const float *src;
+    float *dst;
+    uint64_t floats;
+};
+hipError_t launch_copy_rows(hipStream_t, const CopyRow *table, uint32_t entries);
+// Raises the dynamic LDS limit of the GEMV variants to hold `cols` floats.
+hipError_t configure_gemv(uint64_t max_cols);
+// First maximal index per row (strict >); any NaN gives 0xffffffff.
+hipError_t launch_argmax_rows(hipStream_t, const float *x, uint64_t width, uint64_t rows,
+                              uint32_t *out);
+
+}  // namespace plamo

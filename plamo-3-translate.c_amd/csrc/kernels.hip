@@ -1,0 +1,955 @@
+// gfx950 kernels of the PLaMo-3-Translate token loop.
+//
+// Numerics follow the reference's FP32 path (tests/*_reference.s): BF16
+// weights are widened by a 16-bit shift, every product and sum is FP32, the
+// exponential is the reference's degree-7 polynomial, and RoPE uses separate
+// multiplies and adds. This file is compiled with -ffp-contract=off, so a
+// fused multiply-add appears only where written (__builtin_fmaf). Reduction
+// orders are fixed (wave butterflies, then waves in index order), so results
+// are run-to-run deterministic; they differ from the CPU's sequential order
+// only by FP32 rounding.
+#include "kernels.h"
+
+namespace plamo {
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kThreads = 256;
+
+__device__ __forceinline__ float bf16f(uint32_t bits) { return __uint_as_float(bits << 16); }
+
+// tests/activation_reference.s:6-48.
+__device__ __forceinline__ float plamo_exp(float x) {
+    if (!(x >= -87.0f)) return 0.0f;
+    if (x > 88.0f) return __builtin_inff();
+    float n = __builtin_rintf(x * 1.4426950408889634f);
+    int i = (int)n;
+    float r = __builtin_fmaf(-n, 0.6931471805599453f, x);
+    float p = __builtin_fmaf(0.0001984126984126984f, r, 0.001388888888888889f);
+    p = __builtin_fmaf(p, r, 0.008333333333333333f);
+    p = __builtin_fmaf(p, r, 0.041666666666666664f);
+    p = __builtin_fmaf(p, r, 0.16666666666666666f);
+    p = __builtin_fmaf(p, r, 0.5f);
+    p = __builtin_fmaf(p, r, 1.0f);
+    p = __builtin_fmaf(p, r, 1.0f);
+    return p * __int_as_float((i + 127) << 23);
+}
+
+// Butterfly sum: every lane ends with the same bits.
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+
+// 1 / sqrt(mean(x^2) + 1e-6) for a 256-thread block (tests/rmsnorm_reference.s:8-21
+// arithmetic per element; the sum is a fixed tree).
+__device__ float block_rms_inverse(const float *x, uint32_t n, float *red) {
+    float s = 0.0f;
+    for (uint32_t i = threadIdx.x; i < n; i += kThreads) {
+        float t = x[i] * x[i];
+        s = s + t;
+    }
+    s = wave_sum(s);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
+    __syncthreads();
+    float total = (red[0] + red[1]) + (red[2] + red[3]);
+    __syncthreads();
+    float ms = total / (float)n;
+    ms = ms + 0.000001f;
+    float r = __builtin_sqrtf(ms);
+    return 1.0f / r;
+}
+
+// ---------------------------------------------------------------- RoPE table
+// src/rope_table.s:5-30 with src/trig.s:5-44, evaluated per (row, j) in FP64.
+__global__ __launch_bounds__(kThreads) void rope_table_kernel(const float *freq, float scale,
+                                                              uint32_t half, uint64_t first_row,
+                                                              uint64_t rows, float *table) {
+    uint64_t e = (uint64_t)blockIdx.x * kThreads + threadIdx.x;
+    if (e >= rows * half) return;
+    uint64_t row = first_row + e / half;
+    uint32_t j = (uint32_t)(e % half);
+    float position = (float)row;
+    float angle = freq[j] * position;
+    double a = (double)angle;
+    const double two_pi = 6.283185307179586;
+    double n = __builtin_rint(a / two_pi);
+    double r = __builtin_fma(-n, two_pi, a);
+    double r2 = r * r;
+    double p = 2.8114572543455206e-15;
+    p = __builtin_fma(p, r2, -7.647163731819816e-13);
+    p = __builtin_fma(p, r2, 1.6059043836821613e-10);
+    p = __builtin_fma(p, r2, -2.505210838544172e-08);
+    p = __builtin_fma(p, r2, 2.7557319223985893e-06);
+    p = __builtin_fma(p, r2, -0.0001984126984126984);
+    p = __builtin_fma(p, r2, 0.008333333333333333);
+    p = __builtin_fma(p, r2, -0.16666666666666666);
+    p = __builtin_fma(p, r2, 1.0);
+    float s = (float)(p * r);
+    p = 4.779477332387385e-14;
+    p = __builtin_fma(p, r2, -1.1470745597729725e-11);
+    p = __builtin_fma(p, r2, 2.08767569878681e-09);
+    p = __builtin_fma(p, r2, -2.755731922398589e-07);
+    p = __builtin_fma(p, r2, 2.48015873015873e-05);
+    p = __builtin_fma(p, r2, -0.001388888888888889);
+    p = __builtin_fma(p, r2, 0.041666666666666664);
+    p = __builtin_fma(p, r2, -0.5);
+    p = __builtin_fma(p, r2, 1.0);
+    float c = (float)p;
+    float *out = table + row * 2 * half;
+    out[j] = c * scale;
+    out[half + j] = s * scale;
+}
+
+hipError_t launch_rope_table(hipStream_t stream, const float *freq, float scale, uint32_t half,
+                             uint64_t first_row, uint64_t rows, float *table) {
+    uint64_t n = rows * half;
+    if (!n) return hipSuccess;
+    rope_table_kernel<<<(unsigned)((n + kThreads - 1) / kThreads), kThreads, 0, stream>>>(
+        freq, scale, half, first_row, rows, table);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------- embedding
+// src/token.s:6-33: row gather widened from BF16.
+__global__ __launch_bounds__(kThreads) void embed_kernel(const uint16_t *embedding,
+                                                         const uint32_t *ids,
+                                                         const StepParams *params,
+                                                         uint32_t hidden, float *out) {
+    uint32_t t = blockIdx.y;
+    uint32_t id = ids ? ids[t] : params->token;
+    const uint16_t *row = embedding + (uint64_t)id * hidden;
+    float *o = out + (uint64_t)t * hidden;
+    for (uint32_t i = blockIdx.x * kThreads + threadIdx.x; i < hidden; i += gridDim.x * kThreads)
+        o[i] = bf16f(row[i]);
+}
+
+hipError_t launch_embed(hipStream_t stream, const uint16_t *embedding, const uint32_t *ids,
+                        const StepParams *params, uint32_t tokens, uint32_t hidden, float *out) {
+    unsigned bx = (hidden + kThreads - 1) / kThreads;
+    if (bx > 16) bx = 16;
+    embed_kernel<<<dim3(bx, tokens), kThreads, 0, stream>>>(embedding, ids, params, hidden, out);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------- GEMV
+// Decode projections. The prologue normalizes the input vector into LDS
+// (every block computes the same bits); then each wave streams pairs of BF16
+// rows with 16-byte non-temporal loads, FMA-accumulates against the LDS copy,
+// and butterfly-reduces. With SWIGLU the pair is (gate row r, up row r+half)
+// and the output is silu(gate) * up (tests/activation_reference.s:99-126).
+template <bool VEC, bool SWIGLU>
+__global__ __launch_bounds__(kThreads) void gemv_kernel(const uint16_t *__restrict__ w,
+                                                        uint64_t rows, uint64_t cols,
+                                                        Prologue pro, float *__restrict__ y,
+                                                        uint64_t half) {
+    extern __shared__ float xs[];
+    __shared__ float red[4];
+    const uint32_t n = (uint32_t)cols;
+    if (!pro.w) {
+        for (uint32_t i = threadIdx.x; i < n; i += kThreads) xs[i] = pro.src[i];
+    } else if (pro.branch) {
+        float ib = block_rms_inverse(pro.branch, n, red);
+        for (uint32_t i = threadIdx.x; i < n; i += kThreads) {
+            float b = pro.branch[i] * ib;
+            float scale = bf16f(pro.rw[i]) + pro.roffset;
+            xs[i] = pro.src[i] + b * scale;
+        }
+        __syncthreads();
+        if (blockIdx.x == 0 && pro.state_out)
+            for (uint32_t i = threadIdx.x; i < n; i += kThreads) pro.state_out[i] = xs[i];
+        float is = block_rms_inverse(xs, n, red);
+        for (uint32_t i = threadIdx.x; i < n; i += kThreads) {
+            float scale = bf16f(pro.w[i]) + pro.offset;
+            xs[i] = (xs[i] * is) * scale;
+        }
+    } else {
+        float is = block_rms_inverse(pro.src, n, red);
+        for (uint32_t i = threadIdx.x; i < n; i += kThreads) {
+            float scale = bf16f(pro.w[i]) + pro.offset;
+            xs[i] = (pro.src[i] * is) * scale;
+        }
+    }
+    __syncthreads();
+    if (pro.w && blockIdx.x == 0 && pro.norm_out)
+        for (uint32_t i = threadIdx.x; i < n; i += kThreads) pro.norm_out[i] = xs[i];
+
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint64_t pairs = SWIGLU ? half : (rows + 1) / 2;
+    for (uint64_t p = (uint64_t)blockIdx.x * 4 + wave; p < pairs; p += (uint64_t)gridDim.x * 4) {
+        const uint64_t ra = SWIGLU ? p : 2 * p;
+        const uint64_t rb = SWIGLU ? p + half : 2 * p + 1;
+        const bool has_b = rb < rows;
+        const uint16_t *wa = w + ra * cols;
+        const uint16_t *wb = w + (has_b ? rb : ra) * cols;
+        float acc_a = 0.0f, acc_b = 0.0f;
+        if (VEC) {
+            const uint64_t chunks = cols / 8;
+            const u32x4 *va = (const u32x4 *)wa, *vb = (const u32x4 *)wb;
+            uint64_t c = lane;
+            for (; c + 192 < chunks; c += 256) {
+                u32x4 qa[4], qb[4];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    qa[j] = __builtin_nontemporal_load(va + c + 64 * j);
+                    qb[j] = __builtin_nontemporal_load(vb + c + 64 * j);
+                }
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const f32x4 *xp = (const f32x4 *)(xs + (c + 64 * j) * 8);
+                    f32x4 x0 = xp[0], x1 = xp[1];
+                    float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+                    uint32_t ua[4] = {qa[j].x, qa[j].y, qa[j].z, qa[j].w};
+                    uint32_t ub[4] = {qb[j].x, qb[j].y, qb[j].z, qb[j].w};
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        acc_a = __builtin_fmaf(bf16f(ua[e] & 0xffffu), xv[2 * e], acc_a);
+                        acc_a = __builtin_fmaf(__uint_as_float(ua[e] & 0xffff0000u), xv[2 * e + 1], acc_a);
+                        acc_b = __builtin_fmaf(bf16f(ub[e] & 0xffffu), xv[2 * e], acc_b);
+                        acc_b = __builtin_fmaf(__uint_as_float(ub[e] & 0xffff0000u), xv[2 * e + 1], acc_b);
+                    }
+                }
+            }
+            for (; c < chunks; c += 64) {
+                u32x4 qa = __builtin_nontemporal_load(va + c);
+                u32x4 qb = __builtin_nontemporal_load(vb + c);
+                const f32x4 *xp = (const f32x4 *)(xs + c * 8);
+                f32x4 x0 = xp[0], x1 = xp[1];
+                float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+                uint32_t ua[4] = {qa.x, qa.y, qa.z, qa.w};
+                uint32_t ub[4] = {qb.x, qb.y, qb.z, qb.w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    acc_a = __builtin_fmaf(bf16f(ua[e] & 0xffffu), xv[2 * e], acc_a);
+                    acc_a = __builtin_fmaf(__uint_as_float(ua[e] & 0xffff0000u), xv[2 * e + 1], acc_a);
+                    acc_b = __builtin_fmaf(bf16f(ub[e] & 0xffffu), xv[2 * e], acc_b);
+                    acc_b = __builtin_fmaf(__uint_as_float(ub[e] & 0xffff0000u), xv[2 * e + 1], acc_b);
+                }
+            }
+        } else {
+            for (uint64_t k = lane; k < cols; k += 64) {
+                acc_a = __builtin_fmaf(bf16f(wa[k]), xs[k], acc_a);
+                acc_b = __builtin_fmaf(bf16f(wb[k]), xs[k], acc_b);
+            }
+        }
+        acc_a = wave_sum(acc_a);
+        acc_b = wave_sum(acc_b);
+        if (lane == 0) {
+            if (SWIGLU) {
+                float d = plamo_exp(-acc_a) + 1.0f;
+                y[p] = (acc_a / d) * acc_b;
+            } else {
+                y[ra] = acc_a;
+                if (has_b) y[rb] = acc_b;
+            }
+        }
+    }
+}
+
+hipError_t configure_gemv(uint64_t max_cols) {
+    int lds = (int)(max_cols * sizeof(float));
+    if (lds <= 65536) return hipSuccess;
+    const void *kernels[] = {(const void *)gemv_kernel<true, true>, (const void *)gemv_kernel<true, false>,
+                             (const void *)gemv_kernel<false, true>, (const void *)gemv_kernel<false, false>};
+    for (const void *k : kernels) {
+        hipError_t e = hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
+
+template <bool VEC, bool SWIGLU>
+static hipError_t gemv_variant(hipStream_t stream, const uint16_t *w, uint64_t rows,
+                               uint64_t cols, const Prologue &pro, float *y, uint64_t half,
+                               int blocks_hint) {
+    size_t lds = cols * sizeof(float);
+    uint64_t pairs = SWIGLU ? half : (rows + 1) / 2;
+    uint64_t blocks = (pairs + 3) / 4;
+    if (blocks_hint > 0 && blocks > (uint64_t)blocks_hint) blocks = blocks_hint;
+    if (!blocks) blocks = 1;
+    gemv_kernel<VEC, SWIGLU><<<(unsigned)blocks, kThreads, lds, stream>>>(w, rows, cols, pro, y,
+                                                                          half);
+    return hipGetLastError();
+}
+
+hipError_t launch_gemv(hipStream_t stream, const uint16_t *w, uint64_t rows, uint64_t cols,
+                       const Prologue &pro, float *y, uint64_t swiglu_half, int blocks_hint) {
+    bool vec = cols % 8 == 0 && ((uintptr_t)w & 15) == 0;
+    if (swiglu_half)
+        return vec ? gemv_variant<true, true>(stream, w, rows, cols, pro, y, swiglu_half, blocks_hint)
+                   : gemv_variant<false, true>(stream, w, rows, cols, pro, y, swiglu_half, blocks_hint);
+    return vec ? gemv_variant<true, false>(stream, w, rows, cols, pro, y, 0, blocks_hint)
+               : gemv_variant<false, false>(stream, w, rows, cols, pro, y, 0, blocks_hint);
+}
+
+// ---------------------------------------------------------------- GEMM
+// Prompt / candidate projections on FP32 MFMA (v_mfma_f32_16x16x4_f32).
+// Block tile BM tokens x BN weight rows, K step 32; the BF16 weight panel is
+// widened to FP32 while it is staged into LDS. Operand layout of the 16x16x4
+// instruction: lane l supplies A[l%16][l/16] and B[l/16][l%16] and receives
+// D[4*(l/16)+v][l%16], v = 0..3.
+constexpr int kBK = 32;
+template <int BM, int BN, bool VEC>
+__global__ __launch_bounds__(kThreads) void gemm_kernel(const float *__restrict__ x,
+                                                        uint64_t x_stride,
+                                                        const uint16_t *__restrict__ w,
+                                                        uint64_t rows, uint64_t cols,
+                                                        uint64_t tokens, float *__restrict__ y,
+                                                        uint64_t y_stride) {
+    constexpr int WM = BM >= 32 ? 2 : 1;  // waves along tokens
+    constexpr int WN = 4 / WM;            // waves along rows
+    constexpr int MT = BM / (16 * WM);
+    constexpr int NT = BN / (16 * WN);
+    __shared__ float as[BM][kBK + 1];
+    __shared__ float bs[BN][kBK + 1];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int wm = wave / WN, wn = wave % WN;
+    const uint64_t m0 = (uint64_t)blockIdx.y * BM, n0 = (uint64_t)blockIdx.x * BN;
+    f32x4 acc[MT][NT];
+#pragma unroll
+    for (int i = 0; i < MT; ++i)
+#pragma unroll
+        for (int j = 0; j < NT; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    for (uint64_t k0 = 0; k0 < cols; k0 += kBK) {
+        const bool full_k = k0 + kBK <= cols;
+        for (int i = threadIdx.x; i < BM * (kBK / 4); i += kThreads) {
+            int r = i / (kBK / 4), c = (i % (kBK / 4)) * 4;
+            uint64_t t = m0 + r, k = k0 + c;
+            float v0 = 0, v1 = 0, v2 = 0, v3 = 0;
+            if (t < tokens) {
+                const float *src = x + t * x_stride + k;
+                if (VEC && full_k) {
+                    f32x4 v = *(const f32x4 *)src;
+                    v0 = v.x; v1 = v.y; v2 = v.z; v3 = v.w;
+                } else {
+                    if (k < cols) v0 = src[0];
+                    if (k + 1 < cols) v1 = src[1];
+                    if (k + 2 < cols) v2 = src[2];
+                    if (k + 3 < cols) v3 = src[3];
+                }
+            }
+            as[r][c] = v0; as[r][c + 1] = v1; as[r][c + 2] = v2; as[r][c + 3] = v3;
+        }
+        for (int i = threadIdx.x; i < BN * (kBK / 8); i += kThreads) {
+            int r = i / (kBK / 8), c = (i % (kBK / 8)) * 8;
+            uint64_t row = n0 + r, k = k0 + c;
+            float v[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+            if (row < rows) {
+                const uint16_t *src = w + row * cols + k;
+                if (VEC && full_k) {
+                    u32x4 q = __builtin_nontemporal_load((const u32x4 *)src);
+                    uint32_t u[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        v[2 * e] = bf16f(u[e] & 0xffffu);
+                        v[2 * e + 1] = __uint_as_float(u[e] & 0xffff0000u);
+                    }
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 8; ++e)
+                        if (k + e < cols) v[e] = bf16f(src[e]);
+                }
+            }
+#pragma unroll
+            for (int e = 0; e < 8; ++e) bs[r][c + e] = v[e];
+        }
+        __syncthreads();
+#pragma unroll
+        for (int kk = 0; kk < kBK; kk += 4) {
+            float a[MT], b[NT];
+#pragma unroll
+            for (int i = 0; i < MT; ++i) a[i] = as[wm * (BM / WM) + i * 16 + (lane & 15)][kk + (lane >> 4)];
+#pragma unroll
+            for (int j = 0; j < NT; ++j) b[j] = bs[wn * (BN / WN) + j * 16 + (lane & 15)][kk + (lane >> 4)];
+#pragma unroll
+            for (int i = 0; i < MT; ++i)
+#pragma unroll
+                for (int j = 0; j < NT; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i], b[j], acc[i][j], 0, 0, 0);
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int i = 0; i < MT; ++i)
+#pragma unroll
+        for (int j = 0; j < NT; ++j) {
+            uint64_t col = n0 + wn * (BN / WN) + j * 16 + (lane & 15);
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                uint64_t t = m0 + wm * (BM / WM) + i * 16 + 4 * (lane >> 4) + v;
+                if (t < tokens && col < rows) y[t * y_stride + col] = acc[i][j][v];
+            }
+        }
+}
+
+template <int BM, int BN>
+static hipError_t gemm_variant(hipStream_t stream, const float *x, uint64_t x_stride,
+                               const uint16_t *w, uint64_t rows, uint64_t cols, uint64_t tokens,
+                               float *y, uint64_t y_stride) {
+    dim3 grid((unsigned)((rows + BN - 1) / BN), (unsigned)((tokens + BM - 1) / BM));
+    bool vec = cols % 8 == 0 && x_stride % 4 == 0 && ((uintptr_t)w & 15) == 0 &&
+               ((uintptr_t)x & 15) == 0;
+    if (vec)
+        gemm_kernel<BM, BN, true><<<grid, kThreads, 0, stream>>>(x, x_stride, w, rows, cols,
+                                                                 tokens, y, y_stride);
+    else
+        gemm_kernel<BM, BN, false><<<grid, kThreads, 0, stream>>>(x, x_stride, w, rows, cols,
+                                                                  tokens, y, y_stride);
+    return hipGetLastError();
+}
+
+hipError_t launch_gemm(hipStream_t stream, const float *x, uint64_t x_stride, const uint16_t *w,
+                       uint64_t rows, uint64_t cols, uint64_t tokens, float *y,
+                       uint64_t y_stride) {
+    if (!tokens || !rows) return hipSuccess;
+    if (tokens <= 16) return gemm_variant<16, 64>(stream, x, x_stride, w, rows, cols, tokens, y, y_stride);
+    return gemm_variant<64, 64>(stream, x, x_stride, w, rows, cols, tokens, y, y_stride);
+}
+
+// ---------------------------------------------------------------- row norms
+__global__ __launch_bounds__(kThreads) void norm_rows_kernel(const float *x, uint64_t x_stride,
+                                                             const uint16_t *w, float offset,
+                                                             float *y, uint64_t y_stride,
+                                                             uint32_t width) {
+    __shared__ float red[4];
+    const float *xr = x + blockIdx.x * x_stride;
+    float *yr = y + blockIdx.x * y_stride;
+    float inv = block_rms_inverse(xr, width, red);
+    for (uint32_t i = threadIdx.x; i < width; i += kThreads) {
+        float scale = bf16f(w[i]) + offset;
+        yr[i] = (xr[i] * inv) * scale;
+    }
+}
+
+hipError_t launch_norm_rows(hipStream_t stream, const float *x, uint64_t x_stride,
+                            const uint16_t *w, float offset, float *y, uint64_t y_stride,
+                            uint64_t width, uint64_t rows) {
+    if (!rows) return hipSuccess;
+    norm_rows_kernel<<<(unsigned)rows, kThreads, 0, stream>>>(x, x_stride, w, offset, y, y_stride,
+                                                              (uint32_t)width);
+    return hipGetLastError();
+}
+
+// src/layer.s:33-40 / src/model.s:90-108: state += rms(branch) * (w + offset).
+__global__ __launch_bounds__(kThreads) void residual_rows_kernel(float *state, const float *branch,
+                                                                 const uint16_t *w, float offset,
+                                                                 uint32_t width) {
+    __shared__ float red[4];
+    const float *b = branch + (uint64_t)blockIdx.x * width;
+    float *s = state + (uint64_t)blockIdx.x * width;
+    float inv = block_rms_inverse(b, width, red);
+    for (uint32_t i = threadIdx.x; i < width; i += kThreads) {
+        float scale = bf16f(w[i]) + offset;
+        float v = (b[i] * inv) * scale;
+        s[i] = s[i] + v;
+    }
+}
+
+hipError_t launch_residual_rows(hipStream_t stream, float *state, const float *branch,
+                                const uint16_t *w, float offset, uint64_t width, uint64_t rows) {
+    if (!rows) return hipSuccess;
+    residual_rows_kernel<<<(unsigned)rows, kThreads, 0, stream>>>(state, branch, w, offset,
+                                                                  (uint32_t)width);
+    return hipGetLastError();
+}
+
+__global__ __launch_bounds__(kThreads) void swiglu_rows_kernel(const float *gate_up, float *out,
+                                                               uint64_t intermediate,
+                                                               uint64_t total) {
+    uint64_t e = (uint64_t)blockIdx.x * kThreads + threadIdx.x;
+    if (e >= total) return;
+    uint64_t t = e / intermediate, i = e % intermediate;
+    const float *row = gate_up + t * 2 * intermediate;
+    float g = row[i], u = row[intermediate + i];
+    float d = plamo_exp(-g) + 1.0f;
+    out[e] = (g / d) * u;
+}
+
+hipError_t launch_swiglu_rows(hipStream_t stream, const float *gate_up, float *out,
+                              uint64_t intermediate, uint64_t rows) {
+    uint64_t total = intermediate * rows;
+    if (!total) return hipSuccess;
+    swiglu_rows_kernel<<<(unsigned)((total + kThreads - 1) / kThreads), kThreads, 0, stream>>>(
+        gate_up, out, intermediate, total);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------- QKV post
+// src/qkv.s:36-67 (offset-1 head RMSNorm), src/cache.s:8 (append raw K, V),
+// src/cache_rope.s:44-75 + tests/rope_reference.s:14-30 (rotate).
+__global__ __launch_bounds__(64) void qkv_post_kernel(QkvPost a) {
+    const uint32_t h = blockIdx.x, t = blockIdx.y, lane = threadIdx.x;
+    const uint32_t dim = a.dim, half = dim / 2, width = a.kh * dim;
+    const uint32_t stride = (a.qh + 2 * a.kh) * dim;
+    const float *x = a.qkv + (uint64_t)t * stride + (uint64_t)h * dim;
+    const uint32_t count0 = a.params ? a.params->count[a.layer] : 0;
+    uint32_t position = count0 + t;
+    if (position > a.capacity - 1) position = a.capacity - 1;
+    float s = 0.0f;
+    for (uint32_t i = lane; i < dim; i += 64) {
+        float v = x[i] * x[i];
+        s = s + v;
+    }
+    s = wave_sum(s);
+    float ms = s / (float)dim;
+    ms = ms + 0.000001f;
+    float inv = 1.0f / __builtin_sqrtf(ms);
+    const uint16_t *nw = h < a.qh ? a.qn : a.kn;
+    const float *cs = a.table + (uint64_t)position * dim;
+    const bool last = t + 1 == a.tokens;
+    for (uint32_t j = lane; j < half; j += 64) {
+        float sa = bf16f(nw[j]) + 1.0f, sb = bf16f(nw[j + half]) + 1.0f;
+        float va = (x[j] * inv) * sa;
+        float vb = (x[j + half] * inv) * sb;
+        float c = cs[j], sn = cs[half + j];
+        float p0 = va * c, p1 = vb * sn;
+        float ra = p0 - p1;
+        float p2 = vb * c, p3 = va * sn;
+        float rb = p2 + p3;
+        if (h < a.qh) {
+            float *q = a.q_out + (uint64_t)t * a.qh * dim + (uint64_t)h * dim;
+            q[j] = ra;
+            q[j + half] = rb;
+        } else {
+            const uint32_t kv = h - a.qh;
+            const uint64_t row = (a.rows_from_count ? count0 : 0) + t;
+            const uint64_t o = row * width + (uint64_t)kv * dim;
+            const float *vsrc = a.qkv + (uint64_t)t * stride + (uint64_t)(a.qh + a.kh + kv) * dim;
+            float v0 = vsrc[j], v1 = vsrc[j + half];
+            a.k_raw[o + j] = va;
+            a.k_raw[o + j + half] = vb;
+            a.v[o + j] = v0;
+            a.v[o + j + half] = v1;
+            if (a.rotate_k) {
+                a.k_rot[o + j] = ra;
+                a.k_rot[o + j + half] = rb;
+            }
+            if (a.stage && last) {
+                float *st = a.stage + (uint64_t)kv * dim;
+                st[j] = va;
+                st[j + half] = vb;
+                st[width + j] = v0;
+                st[width + j + half] = v1;
+                st[2 * width + j] = ra;
+                st[2 * width + j + half] = rb;
+            }
+        }
+    }
+}
+
+hipError_t launch_qkv_post(hipStream_t stream, const QkvPost &a) {
+    if (!a.tokens) return hipSuccess;
+    qkv_post_kernel<<<dim3(a.qh + a.kh, a.tokens), 64, 0, stream>>>(a);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------- decode attention
+// Flash-decoding over the rotated cache: block (kv head, split) runs one
+// online softmax per wave over its rows for all query heads of the group and
+// writes (max, sum, weighted V) partials; the last block of a kv head merges
+// them. Scores are the FMA dot * 1/sqrt(d) and exponentials use the
+// reference polynomial (tests/attention_reference.s:9-71).
+constexpr int kMaxGroup = 8;
+__global__ __launch_bounds__(kThreads) void decode_attention_kernel(DecodeAttention a) {
+    extern __shared__ float qs[];  // [G][dim]
+    __shared__ int is_last;
+    const uint32_t kvh = blockIdx.x, split = blockIdx.y;
+    const uint32_t G = a.qh / a.kh, dim = a.dim, width = a.kh * dim;
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t n = a.params->count[a.layer] + 1;
+    const uint32_t slots = a.splits * 4;
+    const uint32_t per = (n + slots - 1) / slots;
+    const uint32_t slot = split * 4 + wave;
+    const uint32_t lo = slot * per < n ? slot * per : n;
+    const uint32_t hi = lo + per < n ? lo + per : n;
+    for (uint32_t i = threadIdx.x; i < G * dim; i += kThreads)
+        qs[i] = a.q[(uint64_t)kvh * G * dim + i];
+    __syncthreads();
+    const float scale = 1.0f / __builtin_sqrtf((float)dim);
+    float m[kMaxGroup], l[kMaxGroup], acc[kMaxGroup][4];
+#pragma unroll
+    for (int g = 0; g < kMaxGroup; ++g) {
+        m[g] = -__builtin_inff();
+        l[g] = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[g][e] = 0.0f;
+    }
+    for (uint32_t r = lo; r < hi; ++r) {
+        const float *k = a.k_rot + (uint64_t)r * width + (uint64_t)kvh * dim;
+        const float *v = a.v + (uint64_t)r * width + (uint64_t)kvh * dim;
+        float kv[4], vv[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            uint32_t d = lane + 64 * e;
+            kv[e] = d < dim ? k[d] : 0.0f;
+            vv[e] = d < dim ? v[d] : 0.0f;
+        }
+#pragma unroll
+        for (int g = 0; g < kMaxGroup; ++g) {
+            if (g < (int)G) {
+                float s = 0.0f;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    uint32_t d = lane + 64 * e;
+                    if (d < dim) s = __builtin_fmaf(qs[g * dim + d], kv[e], s);
+                }
+                s = wave_sum(s) * scale;
+                float mn = fmaxf(m[g], s);
+                float corr = plamo_exp(m[g] - mn);
+                float p = plamo_exp(s - mn);
+                l[g] = l[g] * corr + p;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) acc[g][e] = __builtin_fmaf(p, vv[e], acc[g][e] * corr);
+                m[g] = mn;
+            }
+        }
+    }
+    const uint32_t rec = dim + 2;
+#pragma unroll
+    for (int g = 0; g < kMaxGroup; ++g) {
+        if (g < (int)G) {
+            float *out = a.partial + ((uint64_t)(kvh * G + g) * slots + slot) * rec;
+            if (lane == 0) {
+                out[0] = m[g];
+                out[1] = l[g];
+            }
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                uint32_t d = lane + 64 * e;
+                if (d < dim) out[2 + d] = acc[g][e];
+            }
+        }
+    }
+    // Release the partials at device scope (L2s of other XCDs included), then
+    // count the block; the last block acquires and merges.
+    __threadfence();
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint32_t done = atomicAdd(&a.counters[kvh], 1u);
+        is_last = done + 1 == a.splits;
+    }
+    __syncthreads();
+    if (!is_last) return;
+    __threadfence();
+    for (uint32_t i = threadIdx.x; i < G * dim; i += kThreads) {
+        const uint32_t g = i / dim, d = i % dim;
+        const float *base = a.partial + (uint64_t)(kvh * G + g) * slots * rec;
+        float mx = -__builtin_inff();
+        for (uint32_t sI = 0; sI < slots; ++sI) mx = fmaxf(mx, base[sI * rec]);
+        float sum = 0.0f, o = 0.0f;
+        for (uint32_t sI = 0; sI < slots; ++sI) {
+            const float *p = base + sI * rec;
+            float f = plamo_exp(p[0] - mx);
+            sum = __builtin_fmaf(p[1], f, sum);
+            o = __builtin_fmaf(p[2 + d], f, o);
+        }
+        a.out[(uint64_t)(kvh * G + g) * dim + d] = o / sum;
+    }
+    if (threadIdx.x == 0) a.counters[kvh] = 0;
+}
+
+hipError_t launch_decode_attention(hipStream_t stream, const DecodeAttention &a) {
+    uint32_t G = a.qh / a.kh;
+    decode_attention_kernel<<<dim3(a.kh, a.splits), kThreads, G * a.dim * sizeof(float), stream>>>(a);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------- prompt attention
+// Causal attention for a block of up to 16 queries of one head, online softmax
+// over key tiles of 32 rows. Without a window the keys are the materialized
+// rotated rows; with a window (sliding cache overflow) each key is rotated at
+// its position inside the query's window, as the CPU path does after every
+// shift (src/cache_rope.s:15-27 rotates all rows at local positions).
+constexpr int kQT = 16, kKT = 32;
+__global__ __launch_bounds__(kThreads) void prompt_attention_kernel(PromptAttention a) {
+    extern __shared__ float smem[];
+    const uint32_t dim = a.dim, half = dim / 2, width = a.kh * dim;
+    float *qs = smem;                    // [kQT][dim]
+    float *ks = qs + kQT * dim;          // [kKT][dim + 1]
+    float *vs = ks + kKT * (dim + 1);    // [kKT][dim]
+    float *ps = vs + kKT * dim;          // [kQT][kKT]
+    float *corr = ps + kQT * kKT;        // [kQT]
+    float *mrow = corr + kQT;            // [kQT]
+    float *lrow = mrow + kQT;            // [kQT]
+    const uint32_t h = blockIdx.x, kvh = h / (a.qh / a.kh);
+    const uint32_t t0 = blockIdx.y * kQT;
+    const uint32_t nq = a.tokens - t0 < (uint32_t)kQT ? a.tokens - t0 : kQT;
+    for (uint32_t i = threadIdx.x; i < kQT * dim; i += kThreads) {
+        uint32_t q = i / dim, d = i % dim;
+        qs[i] = q < nq ? a.q[(uint64_t)(t0 + q) * a.qh * dim + (uint64_t)h * dim + d] : 0.0f;
+    }
+    if (threadIdx.x < kQT) {
+        mrow[threadIdx.x] = -__builtin_inff();
+        lrow[threadIdx.x] = 0.0f;
+    }
+    // Key range of the block: virtual rows [lo_min, hi_max).
+    const uint32_t hi_max = a.prefix + t0 + nq;
+    uint32_t lo_min = 0;
+    if (a.window && a.prefix + t0 + 1 > a.window) lo_min = a.prefix + t0 + 1 - a.window;
+    const float scale = 1.0f / __builtin_sqrtf((float)dim);
+    // Output ownership: thread -> query tid/16, dims (tid%16) + 16*i.
+    const uint32_t oq = threadIdx.x / 16, od = threadIdx.x % 16;
+    float o[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) o[i] = 0.0f;
+    __syncthreads();
+    for (uint32_t k0 = lo_min; k0 < hi_max; k0 += kKT) {
+        const uint32_t nk = hi_max - k0 < (uint32_t)kKT ? hi_max - k0 : kKT;
+        for (uint32_t i = threadIdx.x; i < kKT * dim; i += kThreads) {
+            uint32_t r = i / dim, d = i % dim;
+            float kvv = 0.0f, vvv = 0.0f;
+            if (r < nk) {
+                uint32_t vrow = k0 + r;
+                const float *kp = vrow < a.prefix ? a.k_cache + (uint64_t)vrow * width
+                                                  : a.k_new + (uint64_t)(vrow - a.prefix) * width;
+                const float *vp = vrow < a.prefix ? a.v_cache + (uint64_t)vrow * width
+                                                  : a.v_new + (uint64_t)(vrow - a.prefix) * width;
+                kvv = kp[(uint64_t)kvh * dim + d];
+                vvv = vp[(uint64_t)kvh * dim + d];
+            }
+            ks[r * (dim + 1) + d] = kvv;
+            vs[r * dim + d] = vvv;
+        }
+        __syncthreads();
+        // Scores: thread -> query tid/16, keys tid%16 and tid%16 + 16.
+        {
+            const uint32_t q = threadIdx.x / 16;
+            const uint32_t t = t0 + q;
+            const uint32_t hi = a.prefix + t + 1;
+            uint32_t lo = 0;
+            if (a.window && hi > a.window) lo = hi - a.window;
+            float sv[2];
+            float tile_max = -__builtin_inff();
+            for (int e = 0; e < 2; ++e) {
+                uint32_t kr = threadIdx.x % 16 + 16 * e, vrow = k0 + kr;
+                float s = -__builtin_inff();
+                if (q < nq && kr < nk && vrow >= lo && vrow < hi) {
+                    const float *qv = qs + q * dim;
+                    const float *kv = ks + kr * (dim + 1);
+                    float acc = 0.0f;
+                    if (a.window) {
+                        const float *cs = a.table + (uint64_t)(vrow - lo) * dim;
+                        for (uint32_t j = 0; j < half; ++j) {
+                            float x0 = kv[j], x1 = kv[j + half], c = cs[j], sn = cs[half + j];
+                            float p0 = x0 * c, p1 = x1 * sn;
+                            float r0 = p0 - p1;
+                            acc = __builtin_fmaf(qv[j], r0, acc);
+                        }
+                        for (uint32_t j = 0; j < half; ++j) {
+                            float x0 = kv[j], x1 = kv[j + half], c = cs[j], sn = cs[half + j];
+                            float p2 = x1 * c, p3 = x0 * sn;
+                            float r1 = p2 + p3;
+                            acc = __builtin_fmaf(qv[j + half], r1, acc);
+                        }
+                    } else {
+                        for (uint32_t j = 0; j < dim; ++j) acc = __builtin_fmaf(qv[j], kv[j], acc);
+                    }
+                    s = acc * scale;
+                }
+                sv[e] = s;
+                tile_max = fmaxf(tile_max, s);
+            }
+            // Reduce over the 16 lanes of this query.
+            for (int off = 8; off > 0; off >>= 1) tile_max = fmaxf(tile_max, __shfl_xor(tile_max, off, 16));
+            float m_old = mrow[q];
+            float m_new = fmaxf(m_old, tile_max);
+            float c = 1.0f, psum = 0.0f;
+            for (int e = 0; e < 2; ++e) {
+                float p = 0.0f;
+                if (m_new != -__builtin_inff() && sv[e] != -__builtin_inff()) p = plamo_exp(sv[e] - m_new);
+                ps[q * kKT + threadIdx.x % 16 + 16 * e] = p;
+                psum += p;
+            }
+            for (int off = 8; off > 0; off >>= 1) psum += __shfl_xor(psum, off, 16);
+            if (m_new != -__builtin_inff()) c = plamo_exp(m_old - m_new);
+            __syncthreads();
+            if (threadIdx.x % 16 == 0) {
+                corr[q] = c;
+                mrow[q] = m_new;
+                lrow[q] = lrow[q] * c + psum;
+            }
+        }
+        __syncthreads();
+        {
+            const float c = corr[oq];
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                uint32_t d = i * 16 + od;
+                if (d < dim) {
+                    float acc = o[i] * c;
+                    for (uint32_t kr = 0; kr < nk; ++kr)
+                        acc = __builtin_fmaf(ps[oq * kKT + kr], vs[kr * dim + d], acc);
+                    o[i] = acc;
+                }
+            }
+        }
+        __syncthreads();
+    }
+    if (oq < nq) {
+        float l = lrow[oq];
+        float *out = a.out + (uint64_t)(t0 + oq) * a.qh * dim + (uint64_t)h * dim;
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+            if (i * 16 + od < dim) out[i * 16 + od] = o[i] / l;
+    }
+}
+
+hipError_t launch_prompt_attention(hipStream_t stream, const PromptAttention &a) {
+    if (!a.tokens) return hipSuccess;
+    size_t lds = (kQT * a.dim + kKT * (a.dim + 1) + kKT * a.dim + kQT * kKT + 3 * kQT) * sizeof(float);
+    dim3 grid(a.qh, (a.tokens + kQT - 1) / kQT);
+    prompt_attention_kernel<<<grid, kThreads, lds, stream>>>(a);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------- rotation maintenance
+__global__ __launch_bounds__(kThreads) void rerotate_kernel(const float *k_raw, float *k_rot,
+                                                            const float *table, uint64_t rows,
+                                                            uint32_t kh, uint32_t dim) {
+    const uint32_t half = dim / 2;
+    uint64_t e = (uint64_t)blockIdx.x * kThreads + threadIdx.x;
+    uint64_t per_row = (uint64_t)kh * half;
+    if (e >= rows * per_row) return;
+    uint64_t row = e / per_row;
+    uint32_t head = (uint32_t)((e % per_row) / half), j = (uint32_t)(e % half);
+    uint64_t o = row * kh * dim + (uint64_t)head * dim;
+    float x0 = k_raw[o + j], x1 = k_raw[o + j + half];
+    const float *cs = table + row * dim;
+    float c = cs[j], s = cs[half + j];
+    float p0 = x0 * c, p1 = x1 * s;
+    float p2 = x1 * c, p3 = x0 * s;
+    k_rot[o + j] = p0 - p1;
+    k_rot[o + j + half] = p2 + p3;
+}
+
+hipError_t launch_rerotate(hipStream_t stream, const float *k_raw, float *k_rot,
+                           const float *table, uint64_t rows, uint32_t kh, uint32_t dim) {
+    uint64_t n = rows * kh * (dim / 2);
+    if (!n) return hipSuccess;
+    rerotate_kernel<<<(unsigned)((n + kThreads - 1) / kThreads), kThreads, 0, stream>>>(
+        k_raw, k_rot, table, rows, kh, dim);
+    return hipGetLastError();
+}
+
+__global__ __launch_bounds__(kThreads) void window_gather_kernel(const float *k_raw, const float *v,
+                                                                 const float *new_k,
+                                                                 const float *new_v,
+                                                                 uint64_t new_stride,
+                                                                 float *scratch, uint64_t prefix,
+                                                                 uint64_t first, uint64_t keep,
+                                                                 uint32_t width) {
+    uint64_t e = (uint64_t)blockIdx.x * kThreads + threadIdx.x;
+    if (e >= keep * width) return;
+    uint64_t i = e / width, c = e % width, vrow = first + i;
+    float kv, vv;
+    if (vrow < prefix) {
+        kv = k_raw[vrow * width + c];
+        vv = v[vrow * width + c];
+    } else {
+        kv = new_k[(vrow - prefix) * new_stride + c];
+        vv = new_v[(vrow - prefix) * new_stride + c];
+    }
+    scratch[e] = kv;
+    scratch[keep * width + e] = vv;
+}
+
+hipError_t launch_window_store(hipStream_t stream, float *k_raw, float *v, float *k_rot,
+                               const float *new_k, const float *new_v, uint64_t new_stride,
+                               const float *table, float *scratch, uint64_t prefix,
+                               uint64_t tokens, uint64_t keep, uint32_t kh, uint32_t dim) {
+    uint32_t width = kh * dim;
+    uint64_t n = keep * width;
+    if (!n) return hipSuccess;
+    uint64_t first = prefix + tokens - keep;
+    unsigned blocks = (unsigned)((n + kThreads - 1) / kThreads);
+    window_gather_kernel<<<blocks, kThreads, 0, stream>>>(k_raw, v, new_k, new_v, new_stride,
+                                                          scratch, prefix, first, keep, width);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    e = hipMemcpyAsync(k_raw, scratch, n * 4, hipMemcpyDeviceToDevice, stream);
+    if (e != hipSuccess) return e;
+    e = hipMemcpyAsync(v, scratch + n, n * 4, hipMemcpyDeviceToDevice, stream);
+    if (e != hipSuccess) return e;
+    return launch_rerotate(stream, k_raw, k_rot, table, keep, kh, dim);
+}
+
+// ---------------------------------------------------------------- row copies
+__global__ __launch_bounds__(kThreads) void copy_rows_kernel(const CopyRow *table) {
+    const CopyRow e = table[blockIdx.y];
+    for (uint64_t i = (uint64_t)blockIdx.x * kThreads + threadIdx.x; i < e.floats;
+         i += (uint64_t)gridDim.x * kThreads)
+        e.dst[i] = e.src[i];
+}
+
+hipError_t launch_copy_rows(hipStream_t stream, const CopyRow *table, uint32_t entries) {
+    if (!entries) return hipSuccess;
+    copy_rows_kernel<<<dim3(8, entries), kThreads, 0, stream>>>(table);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------- argmax
+// src/token.s:37-63: first maximal index; NaN anywhere gives 0xffffffff.
+__global__ __launch_bounds__(kThreads) void argmax_kernel(const float *x, uint64_t width,
+                                                          uint32_t *out) {
+    __shared__ float bv[4];
+    __shared__ uint32_t bi[4];
+    __shared__ int bnan[4];
+    const float *row = x + (uint64_t)blockIdx.x * width;
+    float best = -__builtin_inff();
+    uint32_t index = 0xffffffffu;
+    int nan = 0;
+    for (uint64_t i = threadIdx.x; i < width; i += kThreads) {
+        float v = row[i];
+        if (v != v) nan = 1;
+        else if (index == 0xffffffffu || v > best) {
+            best = v;
+            index = (uint32_t)i;
+        }
+    }
+    for (int o = 32; o > 0; o >>= 1) {
+        float ov = __shfl_xor(best, o, 64);
+        uint32_t oi = __shfl_xor(index, o, 64);
+        nan |= __shfl_xor(nan, o, 64);
+        if (oi != 0xffffffffu && (index == 0xffffffffu || ov > best || (ov == best && oi < index))) {
+            best = ov;
+            index = oi;
+        }
+    }
+    const uint32_t wave = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) {
+        bv[wave] = best;
+        bi[wave] = index;
+        bnan[wave] = nan;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float b = bv[0];
+        uint32_t id = bi[0];
+        int any = bnan[0];
+        for (int w = 1; w < 4; ++w) {
+            any |= bnan[w];
+            if (bi[w] != 0xffffffffu && (id == 0xffffffffu || bv[w] > b || (bv[w] == b && bi[w] < id))) {
+                b = bv[w];
+                id = bi[w];
+            }
+        }
+        out[blockIdx.x] = any ? 0xffffffffu : id;
+    }
+}
+
+hipError_t launch_argmax_rows(hipStream_t stream, const float *x, uint64_t width, uint64_t rows,
+                              uint32_t *out) {
+    if (!rows) return hipSuccess;
+    argmax_kernel<<<(unsigned)rows, kThreads, 0, stream>>>(x, width, out);
+    return hipGetLastError();
+}
+
+}  // namespace plamo

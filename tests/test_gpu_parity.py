@@ -1,0 +1,328 @@
+"""GPU parity: the HIP backend through its C ABI against the CPU oracle.
+
+Restates the reference's GPU-vs-CPU suite (tests/metal_decode.c) with the same
+gate (relative L2 <= 1e-4, max |delta| <= 1e-5 * (1 + max |ref|)) on the
+reference's fixture shapes — odd widths (hidden 7, head_dim 6), a sliding
+layer with capacity 3 so the window shifts every step, growth past 128 rows,
+existing prefixes, stale rotations, request resets — plus verify/commit, the
+granular projection/MLP entry points and the decline/failure contract.
+Every GPU call checks that no CPU fallback or error was counted.
+"""
+
+import ctypes
+
+import numpy as np
+import pytest
+
+from parity import compare, gate, oracle_lib, plamo_hip, say, tiny
+
+pytestmark = pytest.mark.gpu
+
+
+def clean(backend):
+    info = backend.info()
+    assert info.errors == 0, info.note.decode()
+    assert info.cpu_fallbacks == 0
+
+
+SHAPES = [  # (hidden, intermediate, head_dim, global capacity) of tests/metal_decode.c:760-785
+    (7, 11, 6, 4100),
+    (128, 257, 128, 19),
+    (128, 4097, 128, 19),
+    (16, 300, 6, 264),
+]
+
+
+@pytest.mark.parametrize("h,inter,dim,capacity", SHAPES)
+def test_decode_steps(h, inter, dim, capacity):
+    say(f"decode h={h} I={inter} dim={dim} cap={capacity}")
+    s = tiny(h=h, inter=inter, dim=dim, capacity=capacity)
+    a, b = s.instance(), s.instance()
+    be = plamo_hip.Backend(s)
+    try:
+        steps = min(capacity, 140)
+        for step in range(steps):
+            if step == 17:  # stale rotations on both sides (tests/metal_decode.c:700-703)
+                for inst in (a, b):
+                    for i in range(2):
+                        inst.rotation(i).processed_count = 0
+            tok = (step * 7 + 2) % 17
+            assert oracle_lib.forward(b, tok)
+            assert be.forward(a, tok) == 1
+            compare(a, b)
+        clean(be)
+        info = be.info()
+        assert info.fused_decodes == steps and info.command_buffers == steps
+        # A full global cache is a failure without changes (tests/metal_decode.c:720-730).
+        if a.cache(1).count == capacity:
+            snap = a.snapshot()
+            assert be.forward(a, 3) == -1
+            assert a.snapshot()["state"].tobytes() == snap["state"].tobytes()
+    finally:
+        be.close()
+        a.close()
+        b.close()
+        s.close()
+
+
+PROMPTS = [1, 2, 3, 4, 7, 8, 9, 17, 31, 32, 33, 116, 128, 129, 255, 257]
+
+
+@pytest.mark.parametrize("h,inter,dim,capacity", [(7, 11, 6, 600), (128, 257, 128, 300)])
+def test_prefill_then_decode(h, inter, dim, capacity):
+    s = tiny(h=h, inter=inter, dim=dim, capacity=capacity)
+    a, b = s.instance(), s.instance()
+    be = plamo_hip.Backend(s)
+    try:
+        for prefix in (0, 2, 6):
+            for n in PROMPTS:
+                if n + prefix >= capacity:
+                    continue
+                for final_only in (0, 1):
+                    say(f"prefill h={h} prefix={prefix} n={n} final_only={final_only}")
+                    a.reset()
+                    b.reset()
+                    for j in range(prefix):
+                        assert oracle_lib.forward(a, j % 17)
+                        assert oracle_lib.forward(b, j % 17)
+                    for i in range(2):  # rebuild stale prefix rotations
+                        a.rotation(i).processed_count = 0
+                    ids = [(j * 7 + 3) % 17 for j in range(n)]
+                    actual = np.zeros((n, h), np.float32)
+                    expected = np.zeros((n, h), np.float32)
+                    assert be.prefill(a, ids, None if final_only else actual) == 1
+                    assert oracle_lib.prefill(b, ids, expected)
+                    if not final_only:
+                        gate(actual, expected, "all prompt states")
+                    compare(a, b)
+                    assert be.forward(a, 7) == 1
+                    assert oracle_lib.forward(b, 7)
+                    compare(a, b)
+        clean(be)
+    finally:
+        be.close()
+        a.close()
+        b.close()
+        s.close()
+
+
+def test_verify_and_commit():
+    # tests/metal_decode.c:309-365
+    s = tiny(h=128, inter=257, dim=128, capacity=40)
+    a, b = s.instance(), s.instance()
+    be = plamo_hip.Backend(s)
+    try:
+        ids = [(i * 7 + 3) % 17 for i in range(16)]
+        for count in (1, 2, 3, 4, 6, 8, 12, 16):
+            say(f"verify count={count}")
+            b.reset()
+            assert oracle_lib.prefill(b, [2, 5])
+            states, logits, gold = [], [], []
+            for i in range(count):
+                assert oracle_lib.forward(b, ids[i])
+                states.append(b.state().copy())
+                logits.append(b.logits().copy())
+                gold.append(int(np.argmax(b.logits())))
+            a.reset()
+            assert be.prefill(a, [2, 5]) == 1
+            before = a.snapshot()
+            r, nxt = be.verify(a, ids[:count])
+            assert r == 1
+            after = a.snapshot()
+            assert after["state"].tobytes() == before["state"].tobytes()
+            assert after["logits"].tobytes() == before["logits"].tobytes()
+            for la, lb in zip(after["layers"], before["layers"]):
+                assert all(x.tobytes() == y.tobytes() for x, y in zip(la[:3], lb[:3]))
+                assert la[3:] == lb[3:]
+            assert be.commit(a, 1) == 0  # out of order
+            for i in range(count):
+                lg = logits[i]
+                top2 = np.sort(lg)[-2:]
+                if top2[1] - top2[0] >= 1e-3:
+                    assert nxt[i] == gold[i], f"candidate {i}"
+                assert be.commit(a, i) == 1
+                gate(a.state(), states[i], "verified state")
+                gate(a.logits(), logits[i], "verified logits")
+            compare(a, b)
+            assert be.commit(a, count) == 0
+            if count >= 4:
+                b.reset()
+                assert oracle_lib.prefill(b, [2, 5])
+                for i in range(3):
+                    assert oracle_lib.forward(b, ids[i])
+                assert oracle_lib.forward(b, 12)
+                a.reset()
+                assert be.prefill(a, [2, 5]) == 1
+                assert be.verify(a, ids[:count])[0] == 1
+                for i in range(3):
+                    assert be.commit(a, i) == 1
+                assert be.forward(a, 12) == 1
+                assert be.commit(a, 3) == 0
+                compare(a, b)
+        clean(be)
+        assert be.info().verification_batches > 0
+    finally:
+        be.close()
+        a.close()
+        b.close()
+        s.close()
+
+
+def test_verify_through_sliding_window():
+    # Candidates past a full sliding window: commit rebases the window on the device.
+    s = tiny(h=24, inter=40, dim=6, capacity=64)
+    a, b = s.instance(), s.instance()
+    be = plamo_hip.Backend(s)
+    try:
+        ids = [4, 9, 1, 16, 2]
+        a.reset()
+        b.reset()
+        assert be.prefill(a, [3, 8, 11]) == 1
+        assert oracle_lib.prefill(b, [3, 8, 11])
+        assert be.verify(a, ids)[0] == 1
+        for i, t in enumerate(ids):
+            assert oracle_lib.forward(b, t)
+            assert be.commit(a, i) == 1
+            compare(a, b)
+        clean(be)
+    finally:
+        be.close()
+        a.close()
+        b.close()
+        s.close()
+
+
+def test_host_edits_are_uploaded():
+    # Prefix restore (runtime/prompt_cache.c:62-82), draft restore
+    # (runtime/draft.c:256-296: processed_count = 0) and CPU steps between GPU calls.
+    s = tiny(h=128, inter=257, dim=128, capacity=100)
+    a, b = s.instance(), s.instance()
+    be = plamo_hip.Backend(s)
+    try:
+        prefix = [1, 4, 9, 16, 3, 8, 2, 11, 5, 7, 10, 6]
+        assert oracle_lib.prefill(b, prefix)
+        snap = b.snapshot()
+        for request in range(3):
+            say(f"prefix restore request {request}")
+            a.reset()
+            b.reset()
+            a.restore(snap)
+            b.restore(snap)
+            body = [(request * 5 + j) % 17 for j in range(9 + request)]
+            assert be.prefill(a, body) == 1
+            assert oracle_lib.prefill(b, body)
+            compare(a, b)
+            for t in (3, 14):
+                assert be.forward(a, t) == 1
+                assert oracle_lib.forward(b, t)
+                compare(a, b)
+            # A CPU step between GPU steps writes the host KV directly.
+            assert oracle_lib.forward(a, 5) and oracle_lib.forward(b, 5)
+            assert be.forward(a, 6) == 1 and oracle_lib.forward(b, 6)
+            compare(a, b)
+            # Draft-style restore: rows kept, rotations marked stale.
+            for inst in (a, b):
+                for i in range(2):
+                    inst.cache(i).count -= 2
+                    inst.rotation(i).processed_count = 0
+                    inst.rotation(i).scale_bits = 0
+            assert be.forward(a, 9) == 1 and oracle_lib.forward(b, 9)
+            compare(a, b)
+        clean(be)
+    finally:
+        be.close()
+        a.close()
+        b.close()
+        s.close()
+
+
+def test_decline_and_failure_contract():
+    s = tiny(h=24, inter=40, dim=6, capacity=64)
+    a = s.instance()
+    try:
+        be = plamo_hip.Backend(s, memory=2)  # PLAMO_METAL_STREAM: nothing resident
+        snap = a.snapshot()
+        assert be.forward(a, 2) == 0
+        assert be.prefill(a, [2, 5, 9]) == 0
+        assert a.snapshot()["state"].tobytes() == snap["state"].tobytes()
+        be.close()
+        be = plamo_hip.Backend(None)  # no mappings: projections not resident
+        assert be.forward(a, 2) == 0 and a.counts() == [0, 0]
+        states = np.zeros((3, 24), np.float32)
+        assert be.prefill(a, [2, 5, 9], states) == 0 and not states.any()
+        assert be.prefill(a, [2, 5, 17], states) == -1  # id out of range
+        assert be.forward(a, 17) == -1
+        assert a.counts() == [0, 0] and not states.any()
+        assert be.preload(s.mapping.base, s.mapping.bytes) == 1
+        assert be.forward(a, 2) == 1 and a.counts() == [1, 1]
+        r, _ = be.verify(a, [])
+        assert r == 0
+        be.close()
+    finally:
+        a.close()
+        s.close()
+
+
+def test_hooks_and_trampolines(hip):
+    s = tiny(h=24, inter=40, dim=6, capacity=64)
+    a, b = s.instance(), s.instance()
+    try:
+        assert plamo_hip.hook_address("plamo_forward_kernel") == 0
+        be = plamo_hip.Backend(s)
+        assert plamo_hip.hook_address("plamo_forward_kernel") != 0
+        assert plamo_hip.hook_address("plamo_compute_context") == be.handle
+        ids = (ctypes.c_uint32 * 3)(2, 5, 9)
+        assert hip.plamo_prefill(a.model_ptr, ids, 3, None) == 1
+        assert oracle_lib.prefill(b, [2, 5, 9])
+        assert hip.plamo_forward(a.model_ptr, 4) == 1 and oracle_lib.forward(b, 4)
+        compare(a, b)
+        assert hip.plamo_forward(a.model_ptr, 99) == 0  # failed hook is not retried
+        info = be.info()
+        assert info.fused_prefills == 1 and info.fused_decodes == 1
+        be.close()
+        assert plamo_hip.hook_address("plamo_forward_kernel") == 0
+        assert plamo_hip.hook_address("plamo_compute_context") == 0
+    finally:
+        a.close()
+        b.close()
+        s.close()
+
+
+def test_linear_and_mlp_entry_points(oracle):
+    s = tiny(h=128, inter=257, dim=128, capacity=64)
+    a = s.instance()
+    be = plamo_hip.Backend(s)
+    try:
+        layer = a.layer(0)
+        q = layer.mixer.contents.qkv.contents
+        rows, cols = (q.qh + 2 * q.kh) * q.dim, q.hidden
+        rng = np.random.default_rng(1)
+        for tokens in (1, 3, 37):
+            x = rng.standard_normal((tokens, cols)).astype(np.float32)
+            r, y = be.linear(q.weight, x, rows)
+            assert r == 1
+            ref = np.zeros((tokens, rows), np.float32)
+            mm = plamo_hip.Matmul(q.weight, x.ctypes.data_as(plamo_hip.f32p),
+                                  ref.ctypes.data_as(plamo_hip.f32p), rows, cols, tokens, cols,
+                                  rows)
+            oracle.oracle_matmul(ctypes.byref(mm))
+            gate(y, ref, f"linear tokens={tokens}")
+        mlp = layer.mlp.contents
+        for tokens in (1, 5):
+            st = rng.standard_normal((tokens, 128)).astype(np.float32)
+            ref = st.copy()
+            assert be.lib.plamo_metal_mlp(be.handle, ctypes.byref(mlp),
+                                          st.ctypes.data_as(plamo_hip.f32p), tokens) == 1
+            for t in range(tokens):
+                row = ref[t].copy()
+                m2 = plamo_hip.Mlp(row.ctypes.data_as(plamo_hip.f32p), mlp.pre, mlp.post, mlp.gu,
+                                   mlp.down, mlp.normalized, mlp.branch, mlp.scratch, 128,
+                                   mlp.intermediate)
+                oracle.oracle_mlp_branch(ctypes.byref(m2))
+                ref[t] = row
+            gate(st, ref, f"mlp tokens={tokens}")
+        clean(be)
+    finally:
+        be.close()
+        a.close()
+        s.close()
