@@ -9,6 +9,7 @@
 // between calls are detected and uploaded. A decode step is one hipGraph.
 #include "../../include/plamo_backend.h"
 #include "../../include/plamo_compute.h"
+#include "../../include/plamo_diag.h"
 #include "kernels.h"
 
 #include <hip/hip_runtime.h>
@@ -59,6 +60,7 @@ struct Layer {
     uint32_t qh = 0, kh = 0, dim = 0, hidden = 0, inter = 0, width = 0;
     uint64_t capacity = 0;
     bool sliding = false;
+    bool fused = false;  // decode attention fused with the Q/K norm and KV append
     uint32_t rope = 0;
     float *k = nullptr, *v = nullptr, *rot = nullptr;
     uint64_t rows = 0;          // device rows allocated
@@ -339,10 +341,10 @@ int prepare(plamo_metal *m, struct model *model) {
         const struct cache *c = l->mixer->cache;
         const struct rotation *r = l->mixer->rotation;
         const struct mlp *p = l->mlp;
-        // runtime/metal_model.m:223-235, plus this backend's kernel limits
-        // (head_dim <= 256, at most 8 query heads per KV head).
+        // runtime/metal_model.m:223-235, plus this backend's kernel limit
+        // head_dim <= 256.
         if (l->hidden != h || q->hidden != h || p->hidden != h || l->mixer->hidden != h ||
-            !q->kh || !q->qh || q->qh % q->kh || q->qh / q->kh > 8 || !q->dim || q->dim % 2 ||
+            !q->kh || !q->qh || q->qh % q->kh || !q->dim || q->dim % 2 ||
             q->dim > 256 || !c->capacity || c->capacity > UINT32_MAX ||
             c->width != q->kh * q->dim || r->cache != c || r->heads != q->kh ||
             r->dim != q->dim || !p->intermediate || p->intermediate > UINT32_MAX / 2 ||
@@ -359,6 +361,7 @@ int prepare(plamo_metal *m, struct model *model) {
         d.width = (uint32_t)c->width;
         d.capacity = c->capacity;
         d.sliding = c->sliding != 0;
+        d.fused = decode_attention_supported(d.dim, d.qh / d.kh);
         d.pre = l->pre;
         d.post = l->post;
         d.mlp_pre = p->pre;
@@ -464,7 +467,7 @@ int prepare(plamo_metal *m, struct model *model) {
     m->branch = dev_alloc<float>(m, h);
     m->act = dev_alloc<float>(m, m->max_inter);
     m->down_out = dev_alloc<float>(m, h);
-    m->partial = dev_alloc<float>(m, m->max_partial * kDecodeSplits * 4);
+    m->partial = dev_alloc<float>(m, m->max_partial * kDecodeSplits);
     m->counters = dev_alloc<uint32_t>(m, 256);
     m->outbox_floats = V + 2 * h + L * 3 * m->max_width;
     m->outbox = dev_alloc<float>(m, m->outbox_floats);
@@ -606,61 +609,17 @@ int encode_decode(plamo_metal *m, struct model *model, const DecodePlan &plan, i
             HIP_TRY(m, launch_rerotate(s, d.k, d.rot, rope.table, rows, d.kh, d.dim));
             ++n;
         }
-        QkvPost qp{};
-        qp.qkv = m->qkv;
-        qp.q_out = m->q;
-        qp.qn = qn;
-        qp.kn = kn;
-        qp.table = rope.table;
-        qp.params = m->params_dev;
-        qp.layer = (uint32_t)i;
-        qp.qh = d.qh;
-        qp.kh = d.kh;
-        qp.dim = d.dim;
-        qp.tokens = 1;
-        qp.capacity = (uint32_t)d.capacity;
-        qp.stage = stage + i * 3 * m->max_width;
-        if (shift) {
-            qp.k_raw = as<float>(m->p_side_k);
-            qp.v = as<float>(m->p_side_v);
-            qp.k_rot = nullptr;
-            qp.rows_from_count = 0;
-            qp.rotate_k = 0;
-        } else {
-            qp.k_raw = d.k;
-            qp.v = d.v;
-            qp.k_rot = d.rot;
-            qp.rows_from_count = 1;
-            qp.rotate_k = 1;
-        }
-        HIP_TRY(m, launch_qkv_post(s, qp));
-        ++n;
-        if (shift) {
-            PromptAttention pa{};
-            pa.q = m->q;
-            pa.k_cache = d.k;
-            pa.v_cache = d.v;
-            pa.k_new = as<float>(m->p_side_k);
-            pa.v_new = as<float>(m->p_side_v);
-            pa.table = rope.table;
-            pa.out = m->attn;
-            pa.prefix = (uint32_t)d.capacity;
-            pa.tokens = 1;
-            pa.qh = d.qh;
-            pa.kh = d.kh;
-            pa.dim = d.dim;
-            pa.window = (uint32_t)d.capacity;
-            HIP_TRY(m, launch_prompt_attention(s, pa));
-            HIP_TRY(m, launch_window_store(s, d.k, d.v, d.rot, as<float>(m->p_side_k),
-                                           as<float>(m->p_side_v), d.width, rope.table,
-                                           as<float>(m->p_window), d.capacity, 1, d.capacity,
-                                           d.kh, d.dim));
-            n += 3;
-        } else {
+        float *layer_stage = stage + i * 3 * m->max_width;
+        if (!shift && d.fused) {
             DecodeAttention da{};
-            da.q = m->q;
-            da.k_rot = d.rot;
+            da.qkv = m->qkv;
+            da.qn = qn;
+            da.kn = kn;
+            da.table = rope.table;
+            da.k_raw = d.k;
             da.v = d.v;
+            da.k_rot = d.rot;
+            da.stage = layer_stage;
             da.out = m->attn;
             da.partial = m->partial;
             da.counters = m->counters;
@@ -672,6 +631,59 @@ int encode_decode(plamo_metal *m, struct model *model, const DecodePlan &plan, i
             da.splits = kDecodeSplits;
             HIP_TRY(m, launch_decode_attention(s, da));
             ++n;
+        } else {
+            // General path (eager only: its arguments depend on the row count).
+            const uint32_t count = m->params_host->count[i];
+            QkvPost qp{};
+            qp.qkv = m->qkv;
+            qp.q_out = m->q;
+            qp.qn = qn;
+            qp.kn = kn;
+            qp.table = rope.table;
+            qp.params = m->params_dev;
+            qp.layer = (uint32_t)i;
+            qp.qh = d.qh;
+            qp.kh = d.kh;
+            qp.dim = d.dim;
+            qp.tokens = 1;
+            qp.capacity = (uint32_t)d.capacity;
+            qp.stage = layer_stage;
+            qp.k_raw = shift ? as<float>(m->p_side_k) : d.k;
+            qp.v = shift ? as<float>(m->p_side_v) : d.v;
+            qp.k_rot = shift ? nullptr : d.rot;
+            qp.rows_from_count = !shift;
+            qp.rotate_k = !shift;
+            HIP_TRY(m, launch_qkv_post(s, qp));
+            PromptAttention pa{};
+            pa.q = m->q;
+            pa.table = rope.table;
+            pa.out = m->attn;
+            pa.prefix = count;
+            pa.tokens = 1;
+            pa.qh = d.qh;
+            pa.kh = d.kh;
+            pa.dim = d.dim;
+            if (shift) {
+                pa.k_cache = d.k;
+                pa.v_cache = d.v;
+                pa.k_new = as<float>(m->p_side_k);
+                pa.v_new = as<float>(m->p_side_v);
+                pa.window = (uint32_t)d.capacity;
+            } else {
+                pa.k_cache = d.rot;
+                pa.v_cache = d.v;
+                pa.k_new = d.rot + (uint64_t)count * d.width;
+                pa.v_new = d.v + (uint64_t)count * d.width;
+            }
+            HIP_TRY(m, launch_prompt_attention(s, pa));
+            n += 2;
+            if (shift) {
+                HIP_TRY(m, launch_window_store(s, d.k, d.v, d.rot, as<float>(m->p_side_k),
+                                               as<float>(m->p_side_v), d.width, rope.table,
+                                               as<float>(m->p_window), d.capacity, 1, d.capacity,
+                                               d.kh, d.dim));
+                n += 2;
+            }
         }
         Prologue po{};
         po.src = m->attn;
@@ -917,7 +929,7 @@ int plamo_metal_forward(struct plamo_metal *m, struct model *model, uint64_t tok
         Layer &d = m->layers[i];
         const struct cache *c = model->layers[i]->mixer->cache;
         plan.shift[i] = c->count == c->capacity;
-        if (plan.shift[i] || plan.stale[i]) plan.special = true;
+        if (plan.shift[i] || plan.stale[i] || !d.fused) plan.special = true;
         uint64_t rows = std::min<uint64_t>(c->count + 1, c->capacity);
         if (!ensure_kv_rows(m, d, rows) || !ensure_rope_rows(m, m->ropes[d.rope], rows)) return -1;
         m->params_host->count[i] = (uint32_t)c->count;
@@ -947,7 +959,7 @@ int plamo_metal_forward(struct plamo_metal *m, struct model *model, uint64_t tok
             }
             m->graph_epoch = m->epoch;
         }
-        dispatches = (int)(3 + 6 * L);
+        dispatches = (int)(2 + 5 * L);
         if (hipGraphLaunch(m->graph, m->stream) != hipSuccess) {
             (void)hipGetLastError();
             problem(m, "decode graph launch failed");
@@ -1159,15 +1171,33 @@ int run_prompt(plamo_metal *m, struct model *model, const uint32_t *ids, uint64_
             rows = 1;
         }
         float *st = state + first * h;
-        HIP_FAIL(m, launch_gemm(s, attn + first * aw, aw, d.o, h, aw, rows, branch, h));
-        HIP_FAIL(m, launch_residual_rows(s, st, branch, post, kAttentionOffset, h, rows));
-        HIP_FAIL(m, launch_norm_rows(s, st, h, mpre, 1.0f, norm, h, h, rows));
-        HIP_FAIL(m, launch_gemm(s, norm, h, d.gu, 2 * (uint64_t)d.inter, h, rows, gu,
-                               2 * (uint64_t)d.inter));
-        HIP_FAIL(m, launch_swiglu_rows(s, gu, act, d.inter, rows));
-        HIP_FAIL(m, launch_gemm(s, act, d.inter, d.down, h, d.inter, rows, branch, h));
-        HIP_FAIL(m, launch_residual_rows(s, st, branch, mpost, kMlpOffset, h, rows));
-        n += 7;
+        if (rows == 1) {
+            // One row: the decode GEMVs (norm and SwiGLU fused) instead of GEMM tiles.
+            Prologue po{};
+            po.src = attn + first * aw;
+            HIP_FAIL(m, launch_gemv(s, d.o, h, aw, po, branch, 0, 2 * m->cus));
+            HIP_FAIL(m, launch_residual_rows(s, st, branch, post, kAttentionOffset, h, 1));
+            Prologue pg{};
+            pg.src = st;
+            pg.w = mpre;
+            pg.offset = 1.0f;
+            HIP_FAIL(m, launch_gemv(s, d.gu, 2 * (uint64_t)d.inter, h, pg, act, d.inter, 2 * m->cus));
+            Prologue pd{};
+            pd.src = act;
+            HIP_FAIL(m, launch_gemv(s, d.down, h, d.inter, pd, branch, 0, 2 * m->cus));
+            HIP_FAIL(m, launch_residual_rows(s, st, branch, mpost, kMlpOffset, h, 1));
+            n += 5;
+        } else {
+            HIP_FAIL(m, launch_gemm(s, attn + first * aw, aw, d.o, h, aw, rows, branch, h));
+            HIP_FAIL(m, launch_residual_rows(s, st, branch, post, kAttentionOffset, h, rows));
+            HIP_FAIL(m, launch_norm_rows(s, st, h, mpre, 1.0f, norm, h, h, rows));
+            HIP_FAIL(m, launch_gemm(s, norm, h, d.gu, 2 * (uint64_t)d.inter, h, rows, gu,
+                                   2 * (uint64_t)d.inter));
+            HIP_FAIL(m, launch_swiglu_rows(s, gu, act, d.inter, rows));
+            HIP_FAIL(m, launch_gemm(s, act, d.inter, d.down, h, d.inter, rows, branch, h));
+            HIP_FAIL(m, launch_residual_rows(s, st, branch, mpost, kMlpOffset, h, rows));
+            n += 7;
+        }
     }
     if (verify) {
         HIP_FAIL(m, launch_norm_rows(s, state, h, m->final_norm, 1.0f, m->v_norm, h, h, T));
@@ -1420,3 +1450,104 @@ int plamo_metal_mlp(struct plamo_metal *m, const struct mlp *mlp, float *states,
 }
 
 }  // extern "C"
+
+extern "C" int plamo_hip_time_kernel(struct plamo_metal *m, struct model *model, uint64_t layer,
+                                     int which, int reps, double *ms_per_launch,
+                                     double *bytes_per_launch) {
+    if (!m || m->model != model || !model || layer >= model->count || reps < 1 ||
+        !ms_per_launch || !bytes_per_launch || !resolve_layers(m, model))
+        return 0;
+    const uint64_t h = model->hidden;
+    Layer &d = m->layers[layer];
+    const int blocks = 2 * m->cus;
+    hipStream_t s = m->stream;
+    double bytes = 0;
+    // Same arguments as the decode graph uses for this kernel.
+    auto launch = [&]() -> hipError_t {
+        Prologue p{};
+        switch (which) {
+        case PLAMO_HIP_QKV:
+            p.src = m->state_a;
+            p.w = d.norms;
+            p.offset = 1.0f;
+            return launch_gemv(s, d.qkv, (uint64_t)(d.qh + 2 * d.kh) * d.dim, h, p, m->qkv, 0,
+                               blocks);
+        case PLAMO_HIP_O:
+            p.src = m->attn;
+            return launch_gemv(s, d.o, h, (uint64_t)d.qh * d.dim, p, m->branch, 0, blocks);
+        case PLAMO_HIP_GATE_UP:
+            p.src = m->state_a;
+            p.w = d.norms + 2 * h;
+            p.offset = 1.0f;
+            p.branch = m->branch;
+            p.rw = d.norms + h;
+            p.roffset = kAttentionOffset;
+            p.state_out = m->state_b;
+            return launch_gemv(s, d.gu, 2 * (uint64_t)d.inter, h, p, m->act, d.inter, blocks);
+        case PLAMO_HIP_DOWN:
+            p.src = m->act;
+            return launch_gemv(s, d.down, h, d.inter, p, m->down_out, 0, blocks);
+        case PLAMO_HIP_HEAD:
+            p.src = m->state_a;
+            p.w = m->final_norm;
+            p.offset = 1.0f;
+            return launch_gemv(s, m->head, model->vocab, h, p, m->outbox, 0, blocks);
+        default: {
+            if (!d.fused) return hipErrorInvalidValue;
+            DecodeAttention da{};
+            da.qkv = m->qkv;
+            da.qn = d.norms + 4 * h;
+            da.kn = d.norms + 4 * h + d.dim;
+            da.table = m->ropes[d.rope].table;
+            da.k_raw = d.k;
+            da.v = d.v;
+            da.k_rot = d.rot;
+            da.stage = nullptr;
+            da.out = m->attn;
+            da.partial = m->partial;
+            da.counters = m->counters;
+            da.params = m->params_dev;
+            da.layer = (uint32_t)layer;
+            da.qh = d.qh;
+            da.kh = d.kh;
+            da.dim = d.dim;
+            da.splits = kDecodeSplits;
+            return launch_decode_attention(s, da);
+        }
+        }
+    };
+    switch (which) {
+    case PLAMO_HIP_QKV: bytes = 2.0 * (d.qh + 2 * d.kh) * d.dim * h; break;
+    case PLAMO_HIP_O: bytes = 2.0 * h * d.qh * d.dim; break;
+    case PLAMO_HIP_GATE_UP: bytes = 2.0 * 2 * d.inter * h; break;
+    case PLAMO_HIP_DOWN: bytes = 2.0 * d.inter * h; break;
+    case PLAMO_HIP_HEAD: bytes = 2.0 * model->vocab * h; break;
+    case PLAMO_HIP_ATTENTION: {
+        // Rows the kernel reads: the count stored for this layer by the last step.
+        uint64_t rows = (uint64_t)m->params_host->count[layer] + 1;
+        bytes = 2.0 * 4.0 * rows * d.width;
+        break;
+    }
+    default: return 0;
+    }
+    if (launch() != hipSuccess || hipStreamSynchronize(s) != hipSuccess) {
+        (void)hipGetLastError();
+        return problem(m, "timed launch failed");
+    }
+    HIP_TRY(m, hipEventRecord(m->start, s));
+    for (int i = 0; i < reps; ++i)
+        if (launch() != hipSuccess) {
+            (void)hipGetLastError();
+            return problem(m, "timed launch failed");
+        }
+    HIP_TRY(m, hipEventRecord(m->stop, s));
+    HIP_TRY(m, hipEventSynchronize(m->stop));
+    float ms = 0;
+    HIP_TRY(m, hipEventElapsedTime(&ms, m->start, m->stop));
+    *ms_per_launch = ms / reps;
+    *bytes_per_launch = bytes;
+    // The attention kernel re-appended this layer's last row from whatever the
+    // QKV buffer now holds: upload the host rows again at the next call.
+    if (which == PLAMO_HIP_ATTENTION) d.synced = false;
+    return 1;
+}

@@ -71,17 +71,28 @@ struct QkvPost {
 };
 hipError_t launch_qkv_post(hipStream_t, const QkvPost &);
 
-// Decode attention for one token over rows [0, count+1) of the rotated cache.
+// Decode attention for one token, fused with the decode form of QkvPost: each
+// block normalizes and rotates the query heads of its KV head, the block that
+// owns row `count` also normalizes/rotates the new key and appends K, V and
+// rotated K (plus the mirror stage), and every block runs an online softmax
+// over its share of rows [0, count]; the last block of a KV head merges the
+// partials. Requires decode_attention_supported(dim, qh / kh), splits <= 8 and
+// count < capacity (a full sliding window takes the general path). Up to 256
+// rows run in one block per KV head; longer contexts use up to `splits` blocks.
 struct DecodeAttention {
-    const float *q;          // [qh*dim]
-    const float *k_rot, *v;  // cache [rows, kh*dim]
+    const float *qkv;        // [(qh+2kh)*dim] projection output
+    const uint16_t *qn, *kn;
+    const float *table;      // RoPE rows [position][dim]: cos | sin
+    float *k_raw, *v, *k_rot;  // cache rows [rows, kh*dim]
+    float *stage;            // optional [3][kh*dim] copy of the appended row
     float *out;              // [qh*dim]
-    float *partial;          // scratch [qh][splits][dim + 2]
+    float *partial;          // scratch [kh][splits][qh/kh][dim + 2]
     uint32_t *counters;      // [kh] zero-initialized; reset by the kernel
     const StepParams *params;
     uint32_t layer, qh, kh, dim, splits;
 };
 hipError_t launch_decode_attention(hipStream_t, const DecodeAttention &);
+bool decode_attention_supported(uint32_t dim, uint32_t group);
 
 // General causal attention for `tokens` query rows. Key j of query t is the
 // virtual row j of [cache rows 0..prefix) ++ [new rows 0..tokens). With

@@ -67,6 +67,23 @@ __device__ float block_rms_inverse(const float *x, uint32_t n, float *red) {
     return 1.0f / r;
 }
 
+// Same as block_rms_inverse when each thread already holds its partial sum.
+__device__ float block_inverse_from_partial(float s, uint32_t n, float *red) {
+    s = wave_sum(s);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
+    __syncthreads();
+    float total = (red[0] + red[1]) + (red[2] + red[3]);
+    __syncthreads();
+    float ms = total / (float)n;
+    ms = ms + 0.000001f;
+    float r = __builtin_sqrtf(ms);
+    return 1.0f / r;
+}
+
+// Norm inputs a GEMV prologue keeps in registers per thread (vectors up to
+// 256 * kPrologueRegs elements take the one-round-trip path).
+constexpr int kPrologueRegs = 16;
+
 // ---------------------------------------------------------------- RoPE table
 // src/rope_table.s:5-30 with src/trig.s:5-44, evaluated per (row, j) in FP64.
 __global__ __launch_bounds__(kThreads) void rope_table_kernel(const float *freq, float scale,
@@ -153,8 +170,78 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(const uint16_t *__restri
     extern __shared__ float xs[];
     __shared__ float red[4];
     const uint32_t n = (uint32_t)cols;
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint64_t pairs = SWIGLU ? half : (rows + 1) / 2;
+    const uint64_t chunks = cols / 8;
+    const uint64_t step = (uint64_t)gridDim.x * 4;
+    uint64_t p = (uint64_t)blockIdx.x * 4 + wave;
+    // The first batch of this wave's weights is requested before the prologue,
+    // so the norm's reductions overlap the HBM latency.
+    u32x4 qa[4], qb[4];
+    auto load_batch = [&](uint64_t pair, uint64_t c) {
+        const uint64_t ra = SWIGLU ? pair : 2 * pair;
+        const uint64_t rb0 = SWIGLU ? pair + half : 2 * pair + 1;
+        const uint64_t rb = rb0 < rows ? rb0 : ra;
+        const u32x4 *va = (const u32x4 *)(w + ra * cols), *vb = (const u32x4 *)(w + rb * cols);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            if (c + 64 * j < chunks) {
+                qa[j] = __builtin_nontemporal_load(va + c + 64 * j);
+                qb[j] = __builtin_nontemporal_load(vb + c + 64 * j);
+            }
+        }
+    };
+    if (VEC && p < pairs) load_batch(p, lane);
+
     if (!pro.w) {
         for (uint32_t i = threadIdx.x; i < n; i += kThreads) xs[i] = pro.src[i];
+        __syncthreads();
+    } else if (n <= kThreads * kPrologueRegs) {
+        // Every input of the norm is requested at once (one memory round trip).
+        float sv[kPrologueRegs], bv[kPrologueRegs], rv[kPrologueRegs], wv[kPrologueRegs];
+#pragma unroll
+        for (int k = 0; k < kPrologueRegs; ++k) {
+            const uint32_t i = threadIdx.x + k * kThreads;
+            const bool ok = i < n;
+            sv[k] = ok ? pro.src[i] : 0.0f;
+            wv[k] = ok ? bf16f(pro.w[i]) : 0.0f;
+            bv[k] = ok && pro.branch ? pro.branch[i] : 0.0f;
+            rv[k] = ok && pro.branch ? bf16f(pro.rw[i]) : 0.0f;
+        }
+        if (pro.branch) {
+            float ss = 0.0f;
+#pragma unroll
+            for (int k = 0; k < kPrologueRegs; ++k) {
+                float t = bv[k] * bv[k];
+                ss = ss + t;
+            }
+            const float ib = block_inverse_from_partial(ss, n, red);
+#pragma unroll
+            for (int k = 0; k < kPrologueRegs; ++k) {
+                float b = bv[k] * ib;
+                float scale = rv[k] + pro.roffset;
+                sv[k] = sv[k] + b * scale;
+            }
+            if (blockIdx.x == 0 && pro.state_out)
+#pragma unroll
+                for (int k = 0; k < kPrologueRegs; ++k) {
+                    const uint32_t i = threadIdx.x + k * kThreads;
+                    if (i < n) pro.state_out[i] = sv[k];
+                }
+        }
+        float ss = 0.0f;
+#pragma unroll
+        for (int k = 0; k < kPrologueRegs; ++k) {
+            float t = sv[k] * sv[k];
+            ss = ss + t;
+        }
+        const float is = block_inverse_from_partial(ss, n, red);
+#pragma unroll
+        for (int k = 0; k < kPrologueRegs; ++k) {
+            const uint32_t i = threadIdx.x + k * kThreads;
+            if (i < n) xs[i] = (sv[k] * is) * (wv[k] + pro.offset);
+        }
+        __syncthreads();
     } else if (pro.branch) {
         float ib = block_rms_inverse(pro.branch, n, red);
         for (uint32_t i = threadIdx.x; i < n; i += kThreads) {
@@ -170,70 +257,49 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(const uint16_t *__restri
             float scale = bf16f(pro.w[i]) + pro.offset;
             xs[i] = (xs[i] * is) * scale;
         }
+        __syncthreads();
     } else {
         float is = block_rms_inverse(pro.src, n, red);
         for (uint32_t i = threadIdx.x; i < n; i += kThreads) {
             float scale = bf16f(pro.w[i]) + pro.offset;
             xs[i] = (pro.src[i] * is) * scale;
         }
+        __syncthreads();
     }
-    __syncthreads();
     if (pro.w && blockIdx.x == 0 && pro.norm_out)
         for (uint32_t i = threadIdx.x; i < n; i += kThreads) pro.norm_out[i] = xs[i];
 
-    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const uint64_t pairs = SWIGLU ? half : (rows + 1) / 2;
-    for (uint64_t p = (uint64_t)blockIdx.x * 4 + wave; p < pairs; p += (uint64_t)gridDim.x * 4) {
+    bool prefetched = VEC;
+    for (; p < pairs; p += step) {
         const uint64_t ra = SWIGLU ? p : 2 * p;
         const uint64_t rb = SWIGLU ? p + half : 2 * p + 1;
         const bool has_b = rb < rows;
-        const uint16_t *wa = w + ra * cols;
-        const uint16_t *wb = w + (has_b ? rb : ra) * cols;
         float acc_a = 0.0f, acc_b = 0.0f;
         if (VEC) {
-            const uint64_t chunks = cols / 8;
-            const u32x4 *va = (const u32x4 *)wa, *vb = (const u32x4 *)wb;
-            uint64_t c = lane;
-            for (; c + 192 < chunks; c += 256) {
-                u32x4 qa[4], qb[4];
+            for (uint64_t c = lane; c < chunks; c += 256) {
+                if (!prefetched) load_batch(p, c);
+                prefetched = false;
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
-                    qa[j] = __builtin_nontemporal_load(va + c + 64 * j);
-                    qb[j] = __builtin_nontemporal_load(vb + c + 64 * j);
-                }
+                    if (c + 64 * j < chunks) {
+                        const f32x4 *xp = (const f32x4 *)(xs + (c + 64 * j) * 8);
+                        f32x4 x0 = xp[0], x1 = xp[1];
+                        float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+                        uint32_t ua[4] = {qa[j].x, qa[j].y, qa[j].z, qa[j].w};
+                        uint32_t ub[4] = {qb[j].x, qb[j].y, qb[j].z, qb[j].w};
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const f32x4 *xp = (const f32x4 *)(xs + (c + 64 * j) * 8);
-                    f32x4 x0 = xp[0], x1 = xp[1];
-                    float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
-                    uint32_t ua[4] = {qa[j].x, qa[j].y, qa[j].z, qa[j].w};
-                    uint32_t ub[4] = {qb[j].x, qb[j].y, qb[j].z, qb[j].w};
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        acc_a = __builtin_fmaf(bf16f(ua[e] & 0xffffu), xv[2 * e], acc_a);
-                        acc_a = __builtin_fmaf(__uint_as_float(ua[e] & 0xffff0000u), xv[2 * e + 1], acc_a);
-                        acc_b = __builtin_fmaf(bf16f(ub[e] & 0xffffu), xv[2 * e], acc_b);
-                        acc_b = __builtin_fmaf(__uint_as_float(ub[e] & 0xffff0000u), xv[2 * e + 1], acc_b);
+                        for (int e = 0; e < 4; ++e) {
+                            acc_a = __builtin_fmaf(bf16f(ua[e] & 0xffffu), xv[2 * e], acc_a);
+                            acc_a = __builtin_fmaf(__uint_as_float(ua[e] & 0xffff0000u), xv[2 * e + 1], acc_a);
+                            acc_b = __builtin_fmaf(bf16f(ub[e] & 0xffffu), xv[2 * e], acc_b);
+                            acc_b = __builtin_fmaf(__uint_as_float(ub[e] & 0xffff0000u), xv[2 * e + 1], acc_b);
+                        }
                     }
                 }
             }
-            for (; c < chunks; c += 64) {
-                u32x4 qa = __builtin_nontemporal_load(va + c);
-                u32x4 qb = __builtin_nontemporal_load(vb + c);
-                const f32x4 *xp = (const f32x4 *)(xs + c * 8);
-                f32x4 x0 = xp[0], x1 = xp[1];
-                float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
-                uint32_t ua[4] = {qa.x, qa.y, qa.z, qa.w};
-                uint32_t ub[4] = {qb.x, qb.y, qb.z, qb.w};
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    acc_a = __builtin_fmaf(bf16f(ua[e] & 0xffffu), xv[2 * e], acc_a);
-                    acc_a = __builtin_fmaf(__uint_as_float(ua[e] & 0xffff0000u), xv[2 * e + 1], acc_a);
-                    acc_b = __builtin_fmaf(bf16f(ub[e] & 0xffffu), xv[2 * e], acc_b);
-                    acc_b = __builtin_fmaf(__uint_as_float(ub[e] & 0xffff0000u), xv[2 * e + 1], acc_b);
-                }
-            }
         } else {
+            const uint16_t *wa = w + ra * cols;
+            const uint16_t *wb = w + (has_b ? rb : ra) * cols;
             for (uint64_t k = lane; k < cols; k += 64) {
                 acc_a = __builtin_fmaf(bf16f(wa[k]), xs[k], acc_a);
                 acc_b = __builtin_fmaf(bf16f(wb[k]), xs[k], acc_b);
@@ -250,6 +316,115 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(const uint16_t *__restri
                 if (has_b) y[rb] = acc_b;
             }
         }
+    }
+}
+
+// Raw-input projections (attention output, MLP down): each lane keeps its
+// slice of x in registers (KC chunks of 8 columns), WPR waves split a row's
+// columns, and a wave streams U rows at a time. No LDS staging of x, so the
+// 16K-column down projection is not occupancy-limited by LDS.
+template <int KC, int WPR, int U>
+__global__ __launch_bounds__(kThreads) void gemv_reg_kernel(const uint16_t *__restrict__ w,
+                                                            uint64_t rows, uint64_t cols,
+                                                            const float *__restrict__ src,
+                                                            float *__restrict__ y) {
+    constexpr int GROUPS = 4 / WPR;
+    __shared__ float part[4][U];
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t pidx = wave % WPR, grp = wave / WPR;
+    const uint64_t col0 = (uint64_t)pidx * KC * 512 + lane * 8;
+    const uint64_t units = (rows + U - 1) / U;
+    const uint64_t step = (uint64_t)gridDim.x * GROUPS;
+    u32x4 wv[U][KC];
+    auto load = [&](uint64_t unit) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            uint64_t r = unit * U + u;
+            if (r >= rows) r = rows - 1;
+            const u32x4 *p = (const u32x4 *)(w + r * cols + col0);
+#pragma unroll
+            for (int c = 0; c < KC; ++c) wv[u][c] = __builtin_nontemporal_load(p + c * 64);
+        }
+    };
+    const uint64_t ubase = (uint64_t)blockIdx.x * GROUPS;
+    if (ubase + grp < units) load(ubase + grp);
+    float x[KC][8];
+#pragma unroll
+    for (int c = 0; c < KC; ++c) {
+        const f32x4 *xp = (const f32x4 *)(src + col0 + c * 512);
+        f32x4 a = xp[0], b = xp[1];
+        x[c][0] = a.x; x[c][1] = a.y; x[c][2] = a.z; x[c][3] = a.w;
+        x[c][4] = b.x; x[c][5] = b.y; x[c][6] = b.z; x[c][7] = b.w;
+    }
+    for (uint64_t ub = ubase; ub < units; ub += step) {
+        const uint64_t unit = ub + grp;
+        const bool valid = unit < units;
+        if (ub != ubase && valid) load(unit);
+        float acc[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            float a = 0.0f;
+#pragma unroll
+            for (int c = 0; c < KC; ++c) {
+                const uint32_t q[4] = {wv[u][c].x, wv[u][c].y, wv[u][c].z, wv[u][c].w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    a = __builtin_fmaf(bf16f(q[e] & 0xffffu), x[c][2 * e], a);
+                    a = __builtin_fmaf(__uint_as_float(q[e] & 0xffff0000u), x[c][2 * e + 1], a);
+                }
+            }
+            acc[u] = wave_sum(a);
+        }
+        if (WPR == 1) {
+            if (lane == 0 && valid)
+#pragma unroll
+                for (int u = 0; u < U; ++u)
+                    if (unit * U + u < rows) y[unit * U + u] = acc[u];
+        } else {
+            if (lane == 0)
+#pragma unroll
+                for (int u = 0; u < U; ++u) part[wave][u] = acc[u];
+            __syncthreads();
+            if (pidx == 0 && lane == 0 && valid)
+#pragma unroll
+                for (int u = 0; u < U; ++u) {
+                    float t = part[wave][u];
+#pragma unroll
+                    for (int q = 1; q < WPR; ++q) t += part[wave + q][u];
+                    if (unit * U + u < rows) y[unit * U + u] = t;
+                }
+            __syncthreads();
+        }
+    }
+}
+
+// Column counts the register GEMV covers: cols = 512 * KC * WPR.
+template <int KC, int WPR, int U>
+static hipError_t gemv_reg_variant(hipStream_t stream, const uint16_t *w, uint64_t rows,
+                                   uint64_t cols, const float *src, float *y, int blocks_hint) {
+    constexpr int GROUPS = 4 / WPR;
+    uint64_t units = (rows + U - 1) / U;
+    uint64_t blocks = (units + GROUPS - 1) / GROUPS;
+    if (blocks_hint > 0 && blocks > (uint64_t)blocks_hint) blocks = blocks_hint;
+    gemv_reg_kernel<KC, WPR, U><<<(unsigned)blocks, kThreads, 0, stream>>>(w, rows, cols, src, y);
+    return hipGetLastError();
+}
+
+static bool gemv_reg_launch(hipStream_t stream, const uint16_t *w, uint64_t rows, uint64_t cols,
+                            const float *src, float *y, int blocks_hint, hipError_t *status) {
+    if (((uintptr_t)w & 15) || ((uintptr_t)src & 15) || cols % 512) return false;
+    switch (cols / 512) {
+    case 1: *status = gemv_reg_variant<1, 1, 2>(stream, w, rows, cols, src, y, blocks_hint); return true;
+    case 2: *status = gemv_reg_variant<2, 1, 2>(stream, w, rows, cols, src, y, blocks_hint); return true;
+    case 4: *status = gemv_reg_variant<4, 1, 2>(stream, w, rows, cols, src, y, blocks_hint); return true;
+    case 5: *status = gemv_reg_variant<5, 1, 2>(stream, w, rows, cols, src, y, blocks_hint); return true;
+    case 8: *status = gemv_reg_variant<8, 1, 2>(stream, w, rows, cols, src, y, blocks_hint); return true;
+    case 12: *status = gemv_reg_variant<6, 2, 2>(stream, w, rows, cols, src, y, blocks_hint); return true;
+    case 16: *status = gemv_reg_variant<8, 2, 1>(stream, w, rows, cols, src, y, blocks_hint); return true;
+    case 20: *status = gemv_reg_variant<5, 4, 1>(stream, w, rows, cols, src, y, blocks_hint); return true;
+    case 32: *status = gemv_reg_variant<8, 4, 1>(stream, w, rows, cols, src, y, blocks_hint); return true;
+    case 48: *status = gemv_reg_variant<12, 4, 1>(stream, w, rows, cols, src, y, blocks_hint); return true;
+    default: return false;
     }
 }
 
@@ -281,6 +456,9 @@ static hipError_t gemv_variant(hipStream_t stream, const uint16_t *w, uint64_t r
 
 hipError_t launch_gemv(hipStream_t stream, const uint16_t *w, uint64_t rows, uint64_t cols,
                        const Prologue &pro, float *y, uint64_t swiglu_half, int blocks_hint) {
+    hipError_t status;
+    if (!pro.w && !swiglu_half && gemv_reg_launch(stream, w, rows, cols, pro.src, y, blocks_hint, &status))
+        return status;
     bool vec = cols % 8 == 0 && ((uintptr_t)w & 15) == 0;
     if (swiglu_half)
         return vec ? gemv_variant<true, true>(stream, w, rows, cols, pro, y, swiglu_half, blocks_hint)
@@ -552,114 +730,349 @@ hipError_t launch_qkv_post(hipStream_t stream, const QkvPost &a) {
 }
 
 // ---------------------------------------------------------------- decode attention
-// Flash-decoding over the rotated cache: block (kv head, split) runs one
-// online softmax per wave over its rows for all query heads of the group and
-// writes (max, sum, weighted V) partials; the last block of a kv head merges
-// them. Scores are the FMA dot * 1/sqrt(d) and exponentials use the
-// reference polynomial (tests/attention_reference.s:9-71).
+// Flash-decoding with lanes mapped to KV rows: a wave takes up to 64 rows at a
+// time, each lane forms its row's dot products with the group's query heads
+// (FMA chains, tests/attention_reference.s:27-40), the scores go through an
+// online softmax with the reference exponential, and the weights are
+// broadcast with readlane for the V accumulation.
 constexpr int kMaxGroup = 8;
-__global__ __launch_bounds__(kThreads) void decode_attention_kernel(DecodeAttention a) {
-    extern __shared__ float qs[];  // [G][dim]
+
+__device__ __forceinline__ float read_lane(float v, uint32_t lane) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), (int)lane));
+}
+
+// Offset-1 head RMSNorm then split-half rotation (src/qkv.s:36-67,
+// tests/rope_reference.s:14-30) of one head by one wave.
+__device__ __forceinline__ float head_inverse(const float *x, uint32_t dim, uint32_t lane) {
+    float s = 0.0f;
+    for (uint32_t i = lane; i < dim; i += 64) {
+        float t = x[i] * x[i];
+        s = s + t;
+    }
+    s = wave_sum(s);
+    float ms = s / (float)dim;
+    ms = ms + 0.000001f;
+    return 1.0f / __builtin_sqrtf(ms);
+}
+
+// One block of 8 waves per KV head. A wave takes RW rows per pass: for the
+// scores, 16 lanes share a row (DIM/16 dims each, the 16 partial dots are
+// reduced within the 16-lane group) and each lane covers RW/4 rows; for the
+// values, lanes own columns. All K/V loads of a pass are issued together,
+// the first pass's while the query heads are prepared. Contexts longer than
+// kRowsPerBlock rows are split across up to `splits` blocks per KV head and
+// merged by the last one.
+constexpr uint32_t kAttnWaves = 8, kAttnThreads = 64 * kAttnWaves;
+constexpr uint32_t kRowsPerBlock = 1024;
+template <int G>
+constexpr uint32_t attention_rows_per_wave() { return G <= 4 ? 16 : 8; }
+
+template <int DIM, int G>
+__global__ __launch_bounds__(kAttnThreads) void decode_attention_kernel(DecodeAttention a) {
+    constexpr uint32_t kRowsPerWave = attention_rows_per_wave<G>();
+    constexpr uint32_t kRowsPerPass = kAttnWaves * kRowsPerWave;
+    constexpr int PL = DIM / 64;   // value columns per lane
+    constexpr int KD = DIM / 16;   // key dims per lane
+    constexpr int KR = kRowsPerWave / 4;  // key rows per lane
+    constexpr uint32_t rec = DIM + 2;
+    extern __shared__ float smem[];
     __shared__ int is_last;
+    const uint32_t half = DIM / 2, width = a.kh * DIM;
     const uint32_t kvh = blockIdx.x, split = blockIdx.y;
-    const uint32_t G = a.qh / a.kh, dim = a.dim, width = a.kh * dim;
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const uint32_t n = a.params->count[a.layer] + 1;
-    const uint32_t slots = a.splits * 4;
-    const uint32_t per = (n + slots - 1) / slots;
-    const uint32_t slot = split * 4 + wave;
-    const uint32_t lo = slot * per < n ? slot * per : n;
+    float *qs = smem;                          // [G][DIM]
+    float *knew = qs + G * DIM;                // [DIM] rotated new key
+    float *vnew = knew + DIM;                  // [DIM]
+    float *pw = vnew + DIM;                    // [kAttnWaves][kRowsPerWave][G]
+    float *wpart = pw + kAttnWaves * kRowsPerWave * G;  // [kAttnWaves][G][rec]
+
+    const uint32_t count = a.params->count[a.layer];
+    const uint32_t n = count + 1;
+    uint32_t splits = (n + kRowsPerBlock - 1) / kRowsPerBlock;
+    if (splits > a.splits) splits = a.splits;
+    if (split >= splits) return;
+    const uint32_t per = (n + splits - 1) / splits;
+    const uint32_t lo = split * per < n ? split * per : n;
     const uint32_t hi = lo + per < n ? lo + per : n;
-    for (uint32_t i = threadIdx.x; i < G * dim; i += kThreads)
-        qs[i] = a.q[(uint64_t)kvh * G * dim + i];
-    __syncthreads();
-    const float scale = 1.0f / __builtin_sqrtf((float)dim);
-    float m[kMaxGroup], l[kMaxGroup], acc[kMaxGroup][4];
+    const float *kbase = a.k_rot + (uint64_t)kvh * DIM;
+    const float *vbase = a.v + (uint64_t)kvh * DIM;
+    const uint32_t kd0 = (lane & 15) * KD, rg = lane >> 4;
+
+    float kc[KR][KD], vc[kRowsPerWave][PL];
+    auto load_pass = [&](uint32_t base, float (&kr)[KR][KD], float (&vr)[kRowsPerWave][PL]) {
 #pragma unroll
-    for (int g = 0; g < kMaxGroup; ++g) {
+        for (int j = 0; j < KR; ++j) {
+            const uint32_t row = base + rg + 4 * j;
+            if (row < hi && row != count) {
+                const float *k = kbase + (uint64_t)row * width + kd0;
+#pragma unroll
+                for (int i = 0; i < KD; i += 4) {
+                    f32x4 x = *(const f32x4 *)(k + i);
+                    kr[j][i] = x.x;
+                    kr[j][i + 1] = x.y;
+                    kr[j][i + 2] = x.z;
+                    kr[j][i + 3] = x.w;
+                }
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < (int)kRowsPerWave; ++r) {
+            const uint32_t row = base + r;
+            if (row < hi && row != count) {
+                const float *vp = vbase + (uint64_t)row * width;
+#pragma unroll
+                for (int e = 0; e < PL; ++e) vr[r][e] = vp[lane + 64 * e];
+            } else {
+                // Rows past the range get weight 0; their values must be finite.
+#pragma unroll
+                for (int e = 0; e < PL; ++e) vr[r][e] = 0.0f;
+            }
+        }
+    };
+    uint32_t base = lo + wave * kRowsPerWave;
+    load_pass(base, kc, vc);  // in flight while the query heads are prepared
+
+    const float *cs = a.table + (uint64_t)count * DIM;
+    for (uint32_t g = wave; g < (uint32_t)G; g += kAttnWaves) {
+        const float *x = a.qkv + (uint64_t)(kvh * G + g) * DIM;
+        float inv = head_inverse(x, DIM, lane);
+        for (uint32_t j = lane; j < half; j += 64) {
+            float va = (x[j] * inv) * (bf16f(a.qn[j]) + 1.0f);
+            float vb = (x[j + half] * inv) * (bf16f(a.qn[j + half]) + 1.0f);
+            float c = cs[j], sn = cs[half + j];
+            float p0 = va * c, p1 = vb * sn, p2 = vb * c, p3 = va * sn;
+            qs[g * DIM + j] = p0 - p1;
+            qs[g * DIM + j + half] = p2 + p3;
+        }
+    }
+    const bool owner = count >= lo && count < hi;
+    if (owner && wave == kAttnWaves - 1) {
+        const float *x = a.qkv + (uint64_t)(a.qh + kvh) * DIM;
+        const float *vs = a.qkv + (uint64_t)(a.qh + a.kh + kvh) * DIM;
+        float inv = head_inverse(x, DIM, lane);
+        const uint64_t o = (uint64_t)count * width + (uint64_t)kvh * DIM;
+        for (uint32_t j = lane; j < half; j += 64) {
+            float va = (x[j] * inv) * (bf16f(a.kn[j]) + 1.0f);
+            float vb = (x[j + half] * inv) * (bf16f(a.kn[j + half]) + 1.0f);
+            float c = cs[j], sn = cs[half + j];
+            float p0 = va * c, p1 = vb * sn, p2 = vb * c, p3 = va * sn;
+            float ra = p0 - p1, rb = p2 + p3;
+            float v0 = vs[j], v1 = vs[j + half];
+            knew[j] = ra;
+            knew[j + half] = rb;
+            vnew[j] = v0;
+            vnew[j + half] = v1;
+            a.k_raw[o + j] = va;
+            a.k_raw[o + j + half] = vb;
+            a.k_rot[o + j] = ra;
+            a.k_rot[o + j + half] = rb;
+            a.v[o + j] = v0;
+            a.v[o + j + half] = v1;
+            if (a.stage) {
+                float *st = a.stage + (uint64_t)kvh * DIM;
+                st[j] = va;
+                st[j + half] = vb;
+                st[width + j] = v0;
+                st[width + j + half] = v1;
+                st[2 * width + j] = ra;
+                st[2 * width + j + half] = rb;
+            }
+        }
+    }
+    __syncthreads();
+
+    float q[G][KD];
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+        for (int i = 0; i < KD; ++i) q[g][i] = qs[g * DIM + kd0 + i];
+    const float scale = 1.0f / __builtin_sqrtf((float)DIM);
+    float m[G], l[G], acc[G][PL];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
         m[g] = -__builtin_inff();
         l[g] = 0.0f;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) acc[g][e] = 0.0f;
+        for (int e = 0; e < PL; ++e) acc[g][e] = 0.0f;
     }
-    for (uint32_t r = lo; r < hi; ++r) {
-        const float *k = a.k_rot + (uint64_t)r * width + (uint64_t)kvh * dim;
-        const float *v = a.v + (uint64_t)r * width + (uint64_t)kvh * dim;
-        float kv[4], vv[4];
+    float *pwave = pw + wave * kRowsPerWave * G;
+    for (; base < hi; base += kRowsPerPass) {
+        const bool more = base + kRowsPerPass < hi;
+        // The appended row comes from LDS (its global copy is being written).
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            uint32_t d = lane + 64 * e;
-            kv[e] = d < dim ? k[d] : 0.0f;
-            vv[e] = d < dim ? v[d] : 0.0f;
-        }
+        for (int j = 0; j < KR; ++j)
+            if (base + rg + 4 * j == count)
 #pragma unroll
-        for (int g = 0; g < kMaxGroup; ++g) {
-            if (g < (int)G) {
+                for (int i = 0; i < KD; ++i) kc[j][i] = knew[kd0 + i];
+#pragma unroll
+        for (int r = 0; r < (int)kRowsPerWave; ++r)
+            if (base + r == count)
+#pragma unroll
+                for (int e = 0; e < PL; ++e) vc[r][e] = vnew[lane + 64 * e];
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            float sc[KR];
+            float mx = -__builtin_inff();
+#pragma unroll
+            for (int j = 0; j < KR; ++j) {
                 float s = 0.0f;
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    uint32_t d = lane + 64 * e;
-                    if (d < dim) s = __builtin_fmaf(qs[g * dim + d], kv[e], s);
-                }
-                s = wave_sum(s) * scale;
-                float mn = fmaxf(m[g], s);
-                float corr = plamo_exp(m[g] - mn);
-                float p = plamo_exp(s - mn);
-                l[g] = l[g] * corr + p;
+                for (int i = 0; i < KD; ++i) s = __builtin_fmaf(q[g][i], kc[j][i], s);
 #pragma unroll
-                for (int e = 0; e < 4; ++e) acc[g][e] = __builtin_fmaf(p, vv[e], acc[g][e] * corr);
-                m[g] = mn;
+                for (int o = 1; o < 16; o <<= 1) s = s + __shfl_xor(s, o, 64);
+                const bool valid = base + rg + 4 * j < hi;
+                sc[j] = valid ? s * scale : -__builtin_inff();
+                mx = fmaxf(mx, sc[j]);
+            }
+            mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+            mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+            const float mn = fmaxf(m[g], mx);
+            const float corr = plamo_exp(m[g] - mn);
+            float ps = 0.0f;
+#pragma unroll
+            for (int j = 0; j < KR; ++j) {
+                float p = sc[j] == -__builtin_inff() ? 0.0f : plamo_exp(sc[j] - mn);
+                ps += p;
+                if ((lane & 15) == 0) pwave[(rg + 4 * j) * G + g] = p;
+            }
+            ps = ps + __shfl_xor(ps, 16, 64);
+            ps = ps + __shfl_xor(ps, 32, 64);
+            l[g] = l[g] * corr + ps;
+            m[g] = mn;
+#pragma unroll
+            for (int e = 0; e < PL; ++e) acc[g][e] = acc[g][e] * corr;
+        }
+        // The weights written above are read back by every lane of this wave;
+        // LDS operations of one wave complete in order.
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (int r = 0; r < (int)kRowsPerWave; ++r) {
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+                const float pr = pwave[r * G + g];
+#pragma unroll
+                for (int e = 0; e < PL; ++e) acc[g][e] = __builtin_fmaf(pr, vc[r][e], acc[g][e]);
             }
         }
+        __builtin_amdgcn_wave_barrier();
+        if (more) load_pass(base + kRowsPerPass, kc, vc);
     }
-    const uint32_t rec = dim + 2;
+    // Merge the waves in LDS.
 #pragma unroll
-    for (int g = 0; g < kMaxGroup; ++g) {
-        if (g < (int)G) {
-            float *out = a.partial + ((uint64_t)(kvh * G + g) * slots + slot) * rec;
-            if (lane == 0) {
-                out[0] = m[g];
-                out[1] = l[g];
-            }
+    for (int g = 0; g < G; ++g) {
+        float *wp = wpart + (wave * G + g) * rec;
+        if (lane == 0) {
+            wp[0] = m[g];
+            wp[1] = l[g];
+        }
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                uint32_t d = lane + 64 * e;
-                if (d < dim) out[2 + d] = acc[g][e];
+        for (int e = 0; e < PL; ++e) wp[2 + lane + 64 * e] = acc[g][e];
+    }
+    __syncthreads();
+    for (uint32_t i = threadIdx.x; i < G * DIM; i += kAttnThreads) {
+        const uint32_t g = i / DIM, d = i % DIM;
+        float mx = -__builtin_inff();
+#pragma unroll
+        for (uint32_t w = 0; w < kAttnWaves; ++w) mx = fmaxf(mx, wpart[(w * G + g) * rec]);
+        float sum = 0.0f, o = 0.0f;
+#pragma unroll
+        for (uint32_t w = 0; w < kAttnWaves; ++w) {
+            const float *wp = wpart + (w * G + g) * rec;
+            const float f = wp[0] == -__builtin_inff() ? 0.0f : plamo_exp(wp[0] - mx);
+            sum = __builtin_fmaf(wp[1], f, sum);
+            o = __builtin_fmaf(wp[2 + d], f, o);
+        }
+        if (splits == 1) {
+            a.out[(uint64_t)(kvh * G + g) * DIM + d] = o / sum;
+        } else {
+            float *bp = a.partial + ((uint64_t)(kvh * a.splits + split) * G + g) * rec;
+            if (d == 0) {
+                bp[0] = mx;
+                bp[1] = sum;
             }
+            bp[2 + d] = o;
         }
     }
-    // Release the partials at device scope (L2s of other XCDs included), then
-    // count the block; the last block acquires and merges.
+    if (splits == 1) return;
+    // Release the partial at device scope (other XCDs' L2 included), count the
+    // block; the last block of this KV head acquires and merges.
     __threadfence();
     __syncthreads();
     if (threadIdx.x == 0) {
         uint32_t done = atomicAdd(&a.counters[kvh], 1u);
-        is_last = done + 1 == a.splits;
+        is_last = done + 1 == splits;
     }
     __syncthreads();
     if (!is_last) return;
     __threadfence();
-    for (uint32_t i = threadIdx.x; i < G * dim; i += kThreads) {
-        const uint32_t g = i / dim, d = i % dim;
-        const float *base = a.partial + (uint64_t)(kvh * G + g) * slots * rec;
-        float mx = -__builtin_inff();
-        for (uint32_t sI = 0; sI < slots; ++sI) mx = fmaxf(mx, base[sI * rec]);
-        float sum = 0.0f, o = 0.0f;
-        for (uint32_t sI = 0; sI < slots; ++sI) {
-            const float *p = base + sI * rec;
-            float f = plamo_exp(p[0] - mx);
-            sum = __builtin_fmaf(p[1], f, sum);
-            o = __builtin_fmaf(p[2 + d], f, o);
+    for (uint32_t i = threadIdx.x; i < G * DIM; i += kAttnThreads) {
+        const uint32_t g = i / DIM, d = i % DIM;
+        float ms[8], ls[8], os[8];
+#pragma unroll
+        for (int sI = 0; sI < 8; ++sI) {
+            ms[sI] = -__builtin_inff();
+            ls[sI] = 0.0f;
+            os[sI] = 0.0f;
+            if (sI < (int)splits) {
+                const float *bp = a.partial + ((uint64_t)(kvh * a.splits + sI) * G + g) * rec;
+                ms[sI] = bp[0];
+                ls[sI] = bp[1];
+                os[sI] = bp[2 + d];
+            }
         }
-        a.out[(uint64_t)(kvh * G + g) * dim + d] = o / sum;
+        float mx = -__builtin_inff();
+#pragma unroll
+        for (int sI = 0; sI < 8; ++sI) mx = fmaxf(mx, ms[sI]);
+        float sum = 0.0f, o = 0.0f;
+#pragma unroll
+        for (int sI = 0; sI < 8; ++sI) {
+            float f = ms[sI] == -__builtin_inff() ? 0.0f : plamo_exp(ms[sI] - mx);
+            sum = __builtin_fmaf(ls[sI], f, sum);
+            o = __builtin_fmaf(os[sI], f, o);
+        }
+        a.out[(uint64_t)(kvh * G + g) * DIM + d] = o / sum;
     }
     if (threadIdx.x == 0) a.counters[kvh] = 0;
 }
 
-hipError_t launch_decode_attention(hipStream_t stream, const DecodeAttention &a) {
-    uint32_t G = a.qh / a.kh;
-    decode_attention_kernel<<<dim3(a.kh, a.splits), kThreads, G * a.dim * sizeof(float), stream>>>(a);
+bool decode_attention_supported(uint32_t dim, uint32_t group) {
+    return (dim == 64 || dim == 128) &&
+           (group == 1 || group == 2 || group == 4 || group == 6 || group == 8);
+}
+
+static size_t decode_attention_lds(uint32_t dim, uint32_t group) {
+    const uint32_t rows = group <= 4 ? 16 : 8;
+    return (group * dim + 2 * dim + kAttnWaves * rows * group + kAttnWaves * group * (dim + 2)) *
+           sizeof(float);
+}
+
+template <int DIM, int G>
+static hipError_t decode_attention_variant(hipStream_t stream, const DecodeAttention &a) {
+    size_t lds = decode_attention_lds(DIM, G);
+    if (lds > 65536) {
+        hipError_t e = hipFuncSetAttribute((const void *)decode_attention_kernel<DIM, G>,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) return e;
+    }
+    decode_attention_kernel<DIM, G><<<dim3(a.kh, a.splits), kAttnThreads, lds, stream>>>(a);
     return hipGetLastError();
+}
+
+template <int DIM>
+static hipError_t decode_attention_dim(hipStream_t stream, const DecodeAttention &a) {
+    switch (a.qh / a.kh) {
+    case 1: return decode_attention_variant<DIM, 1>(stream, a);
+    case 2: return decode_attention_variant<DIM, 2>(stream, a);
+    case 4: return decode_attention_variant<DIM, 4>(stream, a);
+    case 6: return decode_attention_variant<DIM, 6>(stream, a);
+    default: return decode_attention_variant<DIM, 8>(stream, a);
+    }
+}
+
+hipError_t launch_decode_attention(hipStream_t stream, const DecodeAttention &a) {
+    if (!decode_attention_supported(a.dim, a.qh / a.kh) || a.splits < 1 || a.splits > 8)
+        return hipErrorInvalidValue;
+    return a.dim == 64 ? decode_attention_dim<64>(stream, a) : decode_attention_dim<128>(stream, a);
 }
 
 // ---------------------------------------------------------------- prompt attention

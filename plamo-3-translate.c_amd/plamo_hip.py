@@ -145,12 +145,16 @@ EXPORTS = {
                         "plamo_metal_prepare_model", "plamo_metal_forward",
                         "plamo_metal_prefill", "plamo_metal_verify", "plamo_metal_commit",
                         "plamo_metal_linear", "plamo_metal_mlp"],
+    "plamo_diag.h": ["plamo_hip_time_kernel"],
     "plamo_synthetic.h": ["plamo_synthetic_defaults", "plamo_synthetic_build",
                           "plamo_synthetic_free", "plamo_synthetic_weights",
                           "plamo_synthetic_frequencies", "plamo_synthetic_instantiate",
                           "plamo_synthetic_release", "plamo_synthetic_model",
                           "plamo_synthetic_fill_kv"],
 }
+
+# enum plamo_hip_kernel (include/plamo_diag.h)
+KERNEL_QKV, KERNEL_O, KERNEL_GATE_UP, KERNEL_DOWN, KERNEL_HEAD, KERNEL_ATTENTION = range(6)
 
 _lib = None
 
@@ -183,6 +187,8 @@ def load() -> ctypes.CDLL:
         "plamo_prefill": (c_int, [M, POINTER(c_uint32), c_uint64, f32p]),
         "plamo_argmax": (c_uint64, [f32p, c_uint64]),
         "plamo_register_cpu_path": (None, [POINTER(CpuPath)]),
+        "plamo_hip_time_kernel": (c_int, [c_void_p, M, c_uint64, c_int, c_int,
+                                          POINTER(c_double), POINTER(c_double)]),
         "plamo_synthetic_defaults": (None, [POINTER(SyntheticConfig)] + [c_uint64] * 7),
         "plamo_synthetic_build": (c_void_p, [POINTER(SyntheticConfig), c_uint, c_char_p,
                                              c_size_t]),
@@ -393,6 +399,18 @@ class Backend:
         mm = Matmul(ctypes.cast(weights_ptr, u16p), x.ctypes.data_as(f32p), y.ctypes.data_as(f32p),
                     rows, cols, tokens, cols, rows)
         return self.lib.plamo_metal_linear(self.handle, ctypes.byref(mm)), y
+
+    def maintain(self):
+        """Waits for the backend's stream (runtime/metal.h:51)."""
+        self.lib.plamo_metal_maintain(self.handle)
+
+    def time_kernel(self, inst: Instance, layer: int, which: int, reps: int):
+        """(ms per launch, algorithmic bytes per launch) of one decode kernel."""
+        ms, nbytes = c_double(), c_double()
+        if not self.lib.plamo_hip_time_kernel(self.handle, inst.model_ptr, layer, which, reps,
+                                              ctypes.byref(ms), ctypes.byref(nbytes)):
+            raise RuntimeError(self.info().note.decode())
+        return ms.value, nbytes.value
 
     def close(self):
         if self.handle:

@@ -17,8 +17,10 @@ ABS_SCALE = 1e-5
 
 
 def gate(actual, expected, name):
-    a = np.asarray(actual, dtype=np.float64).ravel()
-    b = np.asarray(expected, dtype=np.float64).ravel()
+    # Copies: a failure report must not touch host arrays freed by the test.
+    a = np.array(actual, dtype=np.float64).ravel()
+    b = np.array(expected, dtype=np.float64).ravel()
+    del actual, expected
     assert np.all(np.isfinite(a)) and np.all(np.isfinite(b)), f"{name}: non-finite values"
     delta = np.abs(a - b)
     norm = float(np.sqrt(np.sum(b * b))) or 1.0
@@ -32,8 +34,8 @@ def gate(actual, expected, name):
 
 def compare(gpu: "plamo_hip.Instance", cpu: "plamo_hip.Instance", kv=True):
     """State, logits, and every layer's K / V / rotated K rows and counters."""
-    gate(gpu.state(), cpu.state(), "state")
-    gate(gpu.logits(), cpu.logits(), "logits")
+    gate(gpu.state().copy(), cpu.state().copy(), "state")
+    gate(gpu.logits().copy(), cpu.logits().copy(), "logits")
     if not kv:
         return
     for i in range(gpu.model.count):
@@ -41,7 +43,7 @@ def compare(gpu: "plamo_hip.Instance", cpu: "plamo_hip.Instance", kv=True):
         assert ca.count == cb.count, f"layer {i}: count {ca.count} vs {cb.count}"
         n = ca.count
         for which in ("k", "v", "rot"):
-            gate(gpu.kv(i, which)[:n], cpu.kv(i, which)[:n], f"layer {i} {which}")
+            gate(gpu.kv(i, which)[:n].copy(), cpu.kv(i, which)[:n].copy(), f"layer {i} {which}")
         ra, rb = gpu.rotation(i), cpu.rotation(i)
         assert ra.processed_count == rb.processed_count, f"layer {i}: processed_count"
         assert ra.scale_bits == rb.scale_bits, f"layer {i}: scale_bits"

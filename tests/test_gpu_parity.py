@@ -141,8 +141,8 @@ def test_verify_and_commit():
                 if top2[1] - top2[0] >= 1e-3:
                     assert nxt[i] == gold[i], f"candidate {i}"
                 assert be.commit(a, i) == 1
-                gate(a.state(), states[i], "verified state")
-                gate(a.logits(), logits[i], "verified logits")
+                gate(a.state().copy(), states[i], "verified state")
+                gate(a.logits().copy(), logits[i], "verified logits")
             compare(a, b)
             assert be.commit(a, count) == 0
             if count >= 4:
