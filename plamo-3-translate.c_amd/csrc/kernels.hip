@@ -14,18 +14,20 @@ namespace plamo {
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kThreads = 256;
 
 __device__ __forceinline__ float bf16f(uint32_t bits) { return __uint_as_float(bits << 16); }
 
 // tests/activation_reference.s:6-48.
+// Branch-free: the polynomial runs on x clamped to [-87, 88] (identical to x
+// inside that range) and the out-of-range results are selected afterwards.
 __device__ __forceinline__ float plamo_exp(float x) {
-    if (!(x >= -87.0f)) return 0.0f;
-    if (x > 88.0f) return __builtin_inff();
-    float n = __builtin_rintf(x * 1.4426950408889634f);
+    const float xc = __builtin_fminf(__builtin_fmaxf(x, -87.0f), 88.0f);
+    float n = __builtin_rintf(xc * 1.4426950408889634f);
     int i = (int)n;
-    float r = __builtin_fmaf(-n, 0.6931471805599453f, x);
+    float r = __builtin_fmaf(-n, 0.6931471805599453f, xc);
     float p = __builtin_fmaf(0.0001984126984126984f, r, 0.001388888888888889f);
     p = __builtin_fmaf(p, r, 0.008333333333333333f);
     p = __builtin_fmaf(p, r, 0.041666666666666664f);
@@ -33,20 +35,51 @@ __device__ __forceinline__ float plamo_exp(float x) {
     p = __builtin_fmaf(p, r, 0.5f);
     p = __builtin_fmaf(p, r, 1.0f);
     p = __builtin_fmaf(p, r, 1.0f);
-    return p * __int_as_float((i + 127) << 23);
+    float v = p * __int_as_float((i + 127) << 23);
+    v = x > 88.0f ? __builtin_inff() : v;
+    return x >= -87.0f ? v : 0.0f;
 }
 
-// Butterfly sum: every lane ends with the same bits.
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+// Cross-lane reductions on DPP (row-local moves, a few cycles each) and
+// readlane, not LDS permutes. Every lane ends with the same bits: each stage
+// adds a value and its partner's, and a + b == b + a.
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+constexpr int kDppSwap1 = 0xB1;        // quad_perm [1,0,3,2]
+constexpr int kDppSwap2 = 0x4E;        // quad_perm [2,3,0,1]
+constexpr int kDppHalfMirror = 0x141;  // lane i <-> 7 - i within 8
+constexpr int kDppMirror = 0x140;      // lane i <-> 15 - i within 16
+
+// Sum over each 16-lane row, in every lane of the row.
+__device__ __forceinline__ float row_sum16(float v) {
+    v = v + dpp<kDppSwap1>(v);
+    v = v + dpp<kDppSwap2>(v);
+    v = v + dpp<kDppHalfMirror>(v);
+    v = v + dpp<kDppMirror>(v);
     return v;
 }
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+__device__ __forceinline__ float row_max16(float v) {
+    v = fmaxf(v, dpp<kDppSwap1>(v));
+    v = fmaxf(v, dpp<kDppSwap2>(v));
+    v = fmaxf(v, dpp<kDppHalfMirror>(v));
+    v = fmaxf(v, dpp<kDppMirror>(v));
     return v;
 }
+__device__ __forceinline__ float lane_value(float v, int lane) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+// Combine the four rows' (row-uniform) values: (r0 + r1) + (r2 + r3).
+__device__ __forceinline__ float rows_sum(float v) {
+    return (lane_value(v, 0) + lane_value(v, 16)) + (lane_value(v, 32) + lane_value(v, 48));
+}
+__device__ __forceinline__ float rows_max(float v) {
+    return fmaxf(fmaxf(lane_value(v, 0), lane_value(v, 16)),
+                 fmaxf(lane_value(v, 32), lane_value(v, 48)));
+}
+__device__ __forceinline__ float wave_sum(float v) { return rows_sum(row_sum16(v)); }
+__device__ __forceinline__ float wave_max(float v) { return rows_max(row_max16(v)); }
 
 // 1 / sqrt(mean(x^2) + 1e-6) for a 256-thread block (tests/rmsnorm_reference.s:8-21
 // arithmetic per element; the sum is a fixed tree).
@@ -80,9 +113,6 @@ __device__ float block_inverse_from_partial(float s, uint32_t n, float *red) {
     return 1.0f / r;
 }
 
-// Norm inputs a GEMV prologue keeps in registers per thread (vectors up to
-// 256 * kPrologueRegs elements take the one-round-trip path).
-constexpr int kPrologueRegs = 16;
 
 // ---------------------------------------------------------------- RoPE table
 // src/rope_table.s:5-30 with src/trig.s:5-44, evaluated per (row, j) in FP64.
@@ -162,6 +192,74 @@ hipError_t launch_embed(hipStream_t stream, const uint16_t *embedding, const uin
 // rows with 16-byte non-temporal loads, FMA-accumulates against the LDS copy,
 // and butterfly-reduces. With SWIGLU the pair is (gate row r, up row r+half)
 // and the output is silu(gate) * up (tests/activation_reference.s:99-126).
+// Loads one batch of a wave's stream: 4 chunks (of 8 BF16 each) per lane of
+// the row pair at iteration `it` (pairs advance every `nb` iterations).
+template <bool SWIGLU>
+__device__ __forceinline__ bool gemv_batch(const uint16_t *w, uint64_t rows, uint64_t cols,
+                                           uint64_t half, uint64_t pairs, uint64_t p0,
+                                           uint64_t step, uint64_t nb, uint64_t it, uint32_t lane,
+                                           u32x4 (&qa)[4], u32x4 (&qb)[4]) {
+    const uint64_t pair = p0 + (it / nb) * step;
+    if (pair >= pairs) return false;
+    const uint64_t chunks = cols / 8, c = lane + (it % nb) * 256;
+    const uint64_t ra = SWIGLU ? pair : 2 * pair;
+    const uint64_t rb0 = SWIGLU ? pair + half : 2 * pair + 1;
+    const uint64_t rb = rb0 < rows ? rb0 : ra;
+    const u32x4 *va = (const u32x4 *)(w + ra * cols), *vb = (const u32x4 *)(w + rb * cols);
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+        if (c + 64 * j < chunks) {
+            qa[j] = __builtin_nontemporal_load(va + c + 64 * j);
+            qb[j] = __builtin_nontemporal_load(vb + c + 64 * j);
+        }
+    return true;
+}
+
+__device__ __forceinline__ void gemv_accumulate(const float *xs, uint64_t chunks, uint64_t c,
+                                                const u32x4 (&qa)[4], const u32x4 (&qb)[4],
+                                                float &acc_a, float &acc_b) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        if (c + 64 * j < chunks) {
+            const f32x4 *xp = (const f32x4 *)(xs + (c + 64 * j) * 8);
+            f32x4 x0 = xp[0], x1 = xp[1];
+            float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+            uint32_t ua[4] = {qa[j].x, qa[j].y, qa[j].z, qa[j].w};
+            uint32_t ub[4] = {qb[j].x, qb[j].y, qb[j].z, qb[j].w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                acc_a = __builtin_fmaf(bf16f(ua[e] & 0xffffu), xv[2 * e], acc_a);
+                acc_a = __builtin_fmaf(__uint_as_float(ua[e] & 0xffff0000u), xv[2 * e + 1], acc_a);
+                acc_b = __builtin_fmaf(bf16f(ub[e] & 0xffffu), xv[2 * e], acc_b);
+                acc_b = __builtin_fmaf(__uint_as_float(ub[e] & 0xffff0000u), xv[2 * e + 1], acc_b);
+            }
+        }
+    }
+}
+
+template <bool SWIGLU>
+__device__ __forceinline__ void gemv_store(float *y, uint64_t rows, uint64_t pair, float acc_a,
+                                           float acc_b, uint32_t lane) {
+    acc_a = wave_sum(acc_a);
+    acc_b = wave_sum(acc_b);
+    if (lane == 0) {
+        if (SWIGLU) {
+            float d = plamo_exp(-acc_a) + 1.0f;
+            y[pair] = (acc_a / d) * acc_b;
+        } else {
+            y[2 * pair] = acc_a;
+            if (2 * pair + 1 < rows) y[2 * pair + 1] = acc_b;
+        }
+    }
+}
+
+// Decode projections with a norm prologue (or a raw input the register GEMV
+// does not cover). Vector-memory loads complete in order on CDNA, so the
+// prologue's own loads are issued first, then the first weight batch, so the
+// norm's reductions overlap the weights in flight. The weight stream is
+// software-pipelined: batch i+1 is requested before batch i is consumed.
+// With SWIGLU the pair is (gate row r, up row r+half) and the output is
+// silu(gate) * up (tests/activation_reference.s:99-126).
 template <bool VEC, bool SWIGLU>
 __global__ __launch_bounds__(kThreads) void gemv_kernel(const uint16_t *__restrict__ w,
                                                         uint64_t rows, uint64_t cols,
@@ -172,85 +270,115 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(const uint16_t *__restri
     const uint32_t n = (uint32_t)cols;
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const uint64_t pairs = SWIGLU ? half : (rows + 1) / 2;
-    const uint64_t chunks = cols / 8;
+    const uint64_t chunks = cols / 8, nb = (chunks + 255) / 256;
     const uint64_t step = (uint64_t)gridDim.x * 4;
-    uint64_t p = (uint64_t)blockIdx.x * 4 + wave;
-    // The first batch of this wave's weights is requested before the prologue,
-    // so the norm's reductions overlap the HBM latency.
-    u32x4 qa[4], qb[4];
-    auto load_batch = [&](uint64_t pair, uint64_t c) {
-        const uint64_t ra = SWIGLU ? pair : 2 * pair;
-        const uint64_t rb0 = SWIGLU ? pair + half : 2 * pair + 1;
-        const uint64_t rb = rb0 < rows ? rb0 : ra;
-        const u32x4 *va = (const u32x4 *)(w + ra * cols), *vb = (const u32x4 *)(w + rb * cols);
+    const uint64_t p0 = (uint64_t)blockIdx.x * 4 + wave;
+    // One-round-trip prologue: contiguous 16-element slices per thread.
+    const bool fast = pro.w && n % 16 == 0 && n <= 16 * kThreads &&
+                      !(((uintptr_t)pro.src | (uintptr_t)pro.w |
+                         (pro.branch ? ((uintptr_t)pro.branch | (uintptr_t)pro.rw) : 0)) & 15);
+    float sv[16], bv[16], wv[16], rv[16];
+    const uint32_t i0 = threadIdx.x * 16;
+    const bool mine = fast && i0 < n;
+    if (mine) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            if (c + 64 * j < chunks) {
-                qa[j] = __builtin_nontemporal_load(va + c + 64 * j);
-                qb[j] = __builtin_nontemporal_load(vb + c + 64 * j);
-            }
+        for (int q = 0; q < 4; ++q) {
+            f32x4 a = *(const f32x4 *)(pro.src + i0 + 4 * q);
+            sv[4 * q] = a.x; sv[4 * q + 1] = a.y; sv[4 * q + 2] = a.z; sv[4 * q + 3] = a.w;
         }
-    };
-    if (VEC && p < pairs) load_batch(p, lane);
-
-    if (!pro.w) {
-        for (uint32_t i = threadIdx.x; i < n; i += kThreads) xs[i] = pro.src[i];
-        __syncthreads();
-    } else if (n <= kThreads * kPrologueRegs) {
-        // Every input of the norm is requested at once (one memory round trip).
-        float sv[kPrologueRegs], bv[kPrologueRegs], rv[kPrologueRegs], wv[kPrologueRegs];
 #pragma unroll
-        for (int k = 0; k < kPrologueRegs; ++k) {
-            const uint32_t i = threadIdx.x + k * kThreads;
-            const bool ok = i < n;
-            sv[k] = ok ? pro.src[i] : 0.0f;
-            wv[k] = ok ? bf16f(pro.w[i]) : 0.0f;
-            bv[k] = ok && pro.branch ? pro.branch[i] : 0.0f;
-            rv[k] = ok && pro.branch ? bf16f(pro.rw[i]) : 0.0f;
+        for (int q = 0; q < 2; ++q) {
+            u32x4 u = *(const u32x4 *)(pro.w + i0 + 8 * q);
+            uint32_t uu[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                wv[8 * q + 2 * e] = bf16f(uu[e] & 0xffffu);
+                wv[8 * q + 2 * e + 1] = __uint_as_float(uu[e] & 0xffff0000u);
+            }
         }
         if (pro.branch) {
-            float ss = 0.0f;
 #pragma unroll
-            for (int k = 0; k < kPrologueRegs; ++k) {
-                float t = bv[k] * bv[k];
+            for (int q = 0; q < 4; ++q) {
+                f32x4 a = *(const f32x4 *)(pro.branch + i0 + 4 * q);
+                bv[4 * q] = a.x; bv[4 * q + 1] = a.y; bv[4 * q + 2] = a.z; bv[4 * q + 3] = a.w;
+            }
+#pragma unroll
+            for (int q = 0; q < 2; ++q) {
+                u32x4 u = *(const u32x4 *)(pro.rw + i0 + 8 * q);
+                uint32_t uu[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    rv[8 * q + 2 * e] = bf16f(uu[e] & 0xffffu);
+                    rv[8 * q + 2 * e + 1] = __uint_as_float(uu[e] & 0xffff0000u);
+                }
+            }
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    u32x4 qa0[4], qb0[4], qa1[4], qb1[4];
+    if (VEC) gemv_batch<SWIGLU>(w, rows, cols, half, pairs, p0, step, nb, 0, lane, qa0, qb0);
+    __builtin_amdgcn_sched_barrier(0);
+
+    if (fast) {
+        float ss = 0.0f;
+        if (pro.branch) {
+            if (mine)
+#pragma unroll
+                for (int k = 0; k < 16; ++k) {
+                    float t = bv[k] * bv[k];
+                    ss = ss + t;
+                }
+            const float ib = block_inverse_from_partial(ss, n, red);
+            if (mine)
+#pragma unroll
+                for (int k = 0; k < 16; ++k) {
+                    float b = bv[k] * ib;
+                    float scale = rv[k] + pro.roffset;
+                    sv[k] = sv[k] + b * scale;
+                }
+            if (blockIdx.x == 0 && pro.state_out && mine)
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                    *(f32x4 *)(pro.state_out + i0 + 4 * q) =
+                        f32x4{sv[4 * q], sv[4 * q + 1], sv[4 * q + 2], sv[4 * q + 3]};
+            ss = 0.0f;
+        }
+        if (mine)
+#pragma unroll
+            for (int k = 0; k < 16; ++k) {
+                float t = sv[k] * sv[k];
                 ss = ss + t;
             }
-            const float ib = block_inverse_from_partial(ss, n, red);
-#pragma unroll
-            for (int k = 0; k < kPrologueRegs; ++k) {
-                float b = bv[k] * ib;
-                float scale = rv[k] + pro.roffset;
-                sv[k] = sv[k] + b * scale;
-            }
-            if (blockIdx.x == 0 && pro.state_out)
-#pragma unroll
-                for (int k = 0; k < kPrologueRegs; ++k) {
-                    const uint32_t i = threadIdx.x + k * kThreads;
-                    if (i < n) pro.state_out[i] = sv[k];
-                }
-        }
-        float ss = 0.0f;
-#pragma unroll
-        for (int k = 0; k < kPrologueRegs; ++k) {
-            float t = sv[k] * sv[k];
-            ss = ss + t;
-        }
         const float is = block_inverse_from_partial(ss, n, red);
+        if (mine)
 #pragma unroll
-        for (int k = 0; k < kPrologueRegs; ++k) {
-            const uint32_t i = threadIdx.x + k * kThreads;
-            if (i < n) xs[i] = (sv[k] * is) * (wv[k] + pro.offset);
-        }
+            for (int q = 0; q < 4; ++q) {
+                f32x4 x;
+                x.x = (sv[4 * q] * is) * (wv[4 * q] + pro.offset);
+                x.y = (sv[4 * q + 1] * is) * (wv[4 * q + 1] + pro.offset);
+                x.z = (sv[4 * q + 2] * is) * (wv[4 * q + 2] + pro.offset);
+                x.w = (sv[4 * q + 3] * is) * (wv[4 * q + 3] + pro.offset);
+                *(f32x4 *)(xs + i0 + 4 * q) = x;
+                if (blockIdx.x == 0 && pro.norm_out) *(f32x4 *)(pro.norm_out + i0 + 4 * q) = x;
+            }
         __syncthreads();
-    } else if (pro.branch) {
-        float ib = block_rms_inverse(pro.branch, n, red);
+    } else if (!pro.w) {
+        for (uint32_t i = threadIdx.x; i < n; i += kThreads) xs[i] = pro.src[i];
+        __syncthreads();
+    } else {
+        float ib = 1.0f;
+        if (pro.branch) ib = block_rms_inverse(pro.branch, n, red);
         for (uint32_t i = threadIdx.x; i < n; i += kThreads) {
-            float b = pro.branch[i] * ib;
-            float scale = bf16f(pro.rw[i]) + pro.roffset;
-            xs[i] = pro.src[i] + b * scale;
+            float v = pro.src[i];
+            if (pro.branch) {
+                float b = pro.branch[i] * ib;
+                float scale = bf16f(pro.rw[i]) + pro.roffset;
+                v = v + b * scale;
+            }
+            xs[i] = v;
         }
         __syncthreads();
-        if (blockIdx.x == 0 && pro.state_out)
+        if (pro.branch && blockIdx.x == 0 && pro.state_out)
             for (uint32_t i = threadIdx.x; i < n; i += kThreads) pro.state_out[i] = xs[i];
         float is = block_rms_inverse(xs, n, red);
         for (uint32_t i = threadIdx.x; i < n; i += kThreads) {
@@ -258,63 +386,40 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(const uint16_t *__restri
             xs[i] = (xs[i] * is) * scale;
         }
         __syncthreads();
-    } else {
-        float is = block_rms_inverse(pro.src, n, red);
-        for (uint32_t i = threadIdx.x; i < n; i += kThreads) {
-            float scale = bf16f(pro.w[i]) + pro.offset;
-            xs[i] = (pro.src[i] * is) * scale;
-        }
-        __syncthreads();
+        if (blockIdx.x == 0 && pro.norm_out)
+            for (uint32_t i = threadIdx.x; i < n; i += kThreads) pro.norm_out[i] = xs[i];
     }
-    if (pro.w && blockIdx.x == 0 && pro.norm_out)
-        for (uint32_t i = threadIdx.x; i < n; i += kThreads) pro.norm_out[i] = xs[i];
 
-    bool prefetched = VEC;
-    for (; p < pairs; p += step) {
-        const uint64_t ra = SWIGLU ? p : 2 * p;
-        const uint64_t rb = SWIGLU ? p + half : 2 * p + 1;
-        const bool has_b = rb < rows;
+    if (VEC) {
         float acc_a = 0.0f, acc_b = 0.0f;
-        if (VEC) {
-            for (uint64_t c = lane; c < chunks; c += 256) {
-                if (!prefetched) load_batch(p, c);
-                prefetched = false;
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    if (c + 64 * j < chunks) {
-                        const f32x4 *xp = (const f32x4 *)(xs + (c + 64 * j) * 8);
-                        f32x4 x0 = xp[0], x1 = xp[1];
-                        float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
-                        uint32_t ua[4] = {qa[j].x, qa[j].y, qa[j].z, qa[j].w};
-                        uint32_t ub[4] = {qb[j].x, qb[j].y, qb[j].z, qb[j].w};
-#pragma unroll
-                        for (int e = 0; e < 4; ++e) {
-                            acc_a = __builtin_fmaf(bf16f(ua[e] & 0xffffu), xv[2 * e], acc_a);
-                            acc_a = __builtin_fmaf(__uint_as_float(ua[e] & 0xffff0000u), xv[2 * e + 1], acc_a);
-                            acc_b = __builtin_fmaf(bf16f(ub[e] & 0xffffu), xv[2 * e], acc_b);
-                            acc_b = __builtin_fmaf(__uint_as_float(ub[e] & 0xffff0000u), xv[2 * e + 1], acc_b);
-                        }
-                    }
-                }
+        for (uint64_t it = 0;; it += 2) {
+            const bool more1 = gemv_batch<SWIGLU>(w, rows, cols, half, pairs, p0, step, nb, it + 1, lane, qa1, qb1);
+            if (p0 + (it / nb) * step >= pairs) break;
+            gemv_accumulate(xs, chunks, lane + (it % nb) * 256, qa0, qb0, acc_a, acc_b);
+            if (it % nb == nb - 1) {
+                gemv_store<SWIGLU>(y, rows, p0 + (it / nb) * step, acc_a, acc_b, lane);
+                acc_a = acc_b = 0.0f;
             }
-        } else {
+            if (!more1) break;
+            gemv_batch<SWIGLU>(w, rows, cols, half, pairs, p0, step, nb, it + 2, lane, qa0, qb0);
+            gemv_accumulate(xs, chunks, lane + ((it + 1) % nb) * 256, qa1, qb1, acc_a, acc_b);
+            if ((it + 1) % nb == nb - 1) {
+                gemv_store<SWIGLU>(y, rows, p0 + ((it + 1) / nb) * step, acc_a, acc_b, lane);
+                acc_a = acc_b = 0.0f;
+            }
+        }
+    } else {
+        for (uint64_t p = p0; p < pairs; p += step) {
+            const uint64_t ra = SWIGLU ? p : 2 * p;
+            const uint64_t rb = SWIGLU ? p + half : 2 * p + 1;
             const uint16_t *wa = w + ra * cols;
-            const uint16_t *wb = w + (has_b ? rb : ra) * cols;
+            const uint16_t *wb = w + (rb < rows ? rb : ra) * cols;
+            float acc_a = 0.0f, acc_b = 0.0f;
             for (uint64_t k = lane; k < cols; k += 64) {
                 acc_a = __builtin_fmaf(bf16f(wa[k]), xs[k], acc_a);
                 acc_b = __builtin_fmaf(bf16f(wb[k]), xs[k], acc_b);
             }
-        }
-        acc_a = wave_sum(acc_a);
-        acc_b = wave_sum(acc_b);
-        if (lane == 0) {
-            if (SWIGLU) {
-                float d = plamo_exp(-acc_a) + 1.0f;
-                y[p] = (acc_a / d) * acc_b;
-            } else {
-                y[ra] = acc_a;
-                if (has_b) y[rb] = acc_b;
-            }
+            gemv_store<SWIGLU>(y, rows, p, acc_a, acc_b, lane);
         }
     }
 }
@@ -730,38 +835,19 @@ hipError_t launch_qkv_post(hipStream_t stream, const QkvPost &a) {
 }
 
 // ---------------------------------------------------------------- decode attention
-// Flash-decoding with lanes mapped to KV rows: a wave takes up to 64 rows at a
-// time, each lane forms its row's dot products with the group's query heads
-// (FMA chains, tests/attention_reference.s:27-40), the scores go through an
-// online softmax with the reference exponential, and the weights are
-// broadcast with readlane for the V accumulation.
-constexpr int kMaxGroup = 8;
-
-__device__ __forceinline__ float read_lane(float v, uint32_t lane) {
-    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), (int)lane));
-}
-
-// Offset-1 head RMSNorm then split-half rotation (src/qkv.s:36-67,
-// tests/rope_reference.s:14-30) of one head by one wave.
-__device__ __forceinline__ float head_inverse(const float *x, uint32_t dim, uint32_t lane) {
-    float s = 0.0f;
-    for (uint32_t i = lane; i < dim; i += 64) {
-        float t = x[i] * x[i];
-        s = s + t;
-    }
-    s = wave_sum(s);
-    float ms = s / (float)dim;
-    ms = ms + 0.000001f;
-    return 1.0f / __builtin_sqrtf(ms);
-}
-
+// Flash-decoding: the group's query heads share one pass over the KV head's
+// rows; scores are FMA chains (tests/attention_reference.s:27-40) and the
+// softmax is online, with the reference exponential.
 // One block of 8 waves per KV head. A wave takes RW rows per pass: for the
 // scores, 16 lanes share a row (DIM/16 dims each, the 16 partial dots are
 // reduced within the 16-lane group) and each lane covers RW/4 rows; for the
-// values, lanes own columns. All K/V loads of a pass are issued together,
-// the first pass's while the query heads are prepared. Contexts longer than
-// kRowsPerBlock rows are split across up to `splits` blocks per KV head and
-// merged by the last one.
+// values, each lane owns DIM/64 adjacent columns. Vector-memory loads return
+// in order, so the loads are issued in the order they are consumed: first
+// what does not depend on the step's row count (query/key heads and norm
+// weights), then the RoPE row, then two passes of K/V rows; pass p+2 is
+// requested before pass p+1 is consumed. Contexts longer than kRowsPerBlock
+// rows are split across up to `splits` blocks per KV head and merged by the
+// last one.
 constexpr uint32_t kAttnWaves = 8, kAttnThreads = 64 * kAttnWaves;
 constexpr uint32_t kRowsPerBlock = 1024;
 template <int G>
@@ -774,17 +860,42 @@ __global__ __launch_bounds__(kAttnThreads) void decode_attention_kernel(DecodeAt
     constexpr int PL = DIM / 64;   // value columns per lane
     constexpr int KD = DIM / 16;   // key dims per lane
     constexpr int KR = kRowsPerWave / 4;  // key rows per lane
+    constexpr uint32_t HALF = DIM / 2;
     constexpr uint32_t rec = DIM + 2;
     extern __shared__ float smem[];
     __shared__ int is_last;
-    const uint32_t half = DIM / 2, width = a.kh * DIM;
+    const uint32_t width = a.kh * DIM;
     const uint32_t kvh = blockIdx.x, split = blockIdx.y;
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     float *qs = smem;                          // [G][DIM]
     float *knew = qs + G * DIM;                // [DIM] rotated new key
     float *vnew = knew + DIM;                  // [DIM]
     float *pw = vnew + DIM;                    // [kAttnWaves][kRowsPerWave][G]
-    float *wpart = pw + kAttnWaves * kRowsPerWave * G;  // [kAttnWaves][G][rec]
+    float *wpart = pw + kAttnWaves * kRowsPerWave * G;  // [kAttnWaves + 1][G][rec]
+
+    // Count-independent operands: wave g < G normalizes query head g, the last
+    // wave the new key; lane j < DIM/2 holds elements j and j + DIM/2.
+    const bool qwave = wave < (uint32_t)G, kwave = wave == kAttnWaves - 1;
+    const bool hl = lane < HALF;
+    float qx[2] = {0.0f, 0.0f}, qw[2] = {0.0f, 0.0f};
+    float kx[2] = {0.0f, 0.0f}, kw[2] = {0.0f, 0.0f}, vx[2] = {0.0f, 0.0f};
+    if (qwave && hl) {
+        const float *x = a.qkv + (uint64_t)(kvh * G + wave) * DIM;
+        qx[0] = x[lane];
+        qx[1] = x[lane + HALF];
+        qw[0] = bf16f(a.qn[lane]);
+        qw[1] = bf16f(a.qn[lane + HALF]);
+    }
+    if (kwave && hl) {
+        const float *x = a.qkv + (uint64_t)(a.qh + kvh) * DIM;
+        const float *vs = a.qkv + (uint64_t)(a.qh + a.kh + kvh) * DIM;
+        kx[0] = x[lane];
+        kx[1] = x[lane + HALF];
+        kw[0] = bf16f(a.kn[lane]);
+        kw[1] = bf16f(a.kn[lane + HALF]);
+        vx[0] = vs[lane];
+        vx[1] = vs[lane + HALF];
+    }
 
     const uint32_t count = a.params->count[a.layer];
     const uint32_t n = count + 1;
@@ -794,98 +905,117 @@ __global__ __launch_bounds__(kAttnThreads) void decode_attention_kernel(DecodeAt
     const uint32_t per = (n + splits - 1) / splits;
     const uint32_t lo = split * per < n ? split * per : n;
     const uint32_t hi = lo + per < n ? lo + per : n;
+    const bool owner = count >= lo && count < hi;
+    // Cached rows of this block; the appended row (index count, the last one)
+    // joins in the merge as one more partial.
+    const uint32_t hr = hi < count ? hi : count;
+    float rc = 0.0f, rs = 0.0f;
+    if ((qwave || (kwave && owner)) && hl) {
+        const float *cs = a.table + (uint64_t)count * DIM;
+        rc = cs[lane];
+        rs = cs[HALF + lane];
+    }
+
     const float *kbase = a.k_rot + (uint64_t)kvh * DIM;
     const float *vbase = a.v + (uint64_t)kvh * DIM;
     const uint32_t kd0 = (lane & 15) * KD, rg = lane >> 4;
-
-    float kc[KR][KD], vc[kRowsPerWave][PL];
+    // Every lane loads unconditionally, also past the range (rows clamped to
+    // the last cached row; their scores are masked, so their weight is 0):
+    // branches around loads make the compiler wait for every load in flight
+    // where paths merge. Addresses are a wave-uniform row base plus a small
+    // lane byte offset.
+    const uint32_t last = hr > 0 ? hr - 1 : 0;
+    const uint32_t koff = (rg * width + kd0) * 4, voff = lane * PL * 4;
     auto load_pass = [&](uint32_t base, float (&kr)[KR][KD], float (&vr)[kRowsPerWave][PL]) {
 #pragma unroll
         for (int j = 0; j < KR; ++j) {
-            const uint32_t row = base + rg + 4 * j;
-            if (row < hi && row != count) {
-                const float *k = kbase + (uint64_t)row * width + kd0;
+            // Row base + rg + 4j, clamped: the lane offset of rg is dropped
+            // when the row would pass `last`.
+            const uint32_t row = base + 4 * j;
+            const uint32_t mine = row + rg <= last ? koff : kd0 * 4;
+            const char *k = (const char *)(kbase + (uint64_t)min(row, last) * width) + mine;
 #pragma unroll
-                for (int i = 0; i < KD; i += 4) {
-                    f32x4 x = *(const f32x4 *)(k + i);
-                    kr[j][i] = x.x;
-                    kr[j][i + 1] = x.y;
-                    kr[j][i + 2] = x.z;
-                    kr[j][i + 3] = x.w;
-                }
+            for (int i = 0; i < KD; i += 4) {
+                f32x4 x = *(const f32x4 *)(k + 4 * i);
+                kr[j][i] = x.x;
+                kr[j][i + 1] = x.y;
+                kr[j][i + 2] = x.z;
+                kr[j][i + 3] = x.w;
             }
         }
 #pragma unroll
         for (int r = 0; r < (int)kRowsPerWave; ++r) {
-            const uint32_t row = base + r;
-            if (row < hi && row != count) {
-                const float *vp = vbase + (uint64_t)row * width;
-#pragma unroll
-                for (int e = 0; e < PL; ++e) vr[r][e] = vp[lane + 64 * e];
+            const char *vp = (const char *)(vbase + (uint64_t)min(base + r, last) * width) + voff;
+            if (PL == 2) {
+                f32x2 x = *(const f32x2 *)vp;
+                vr[r][0] = x.x;
+                vr[r][PL - 1] = x.y;
             } else {
-                // Rows past the range get weight 0; their values must be finite.
 #pragma unroll
-                for (int e = 0; e < PL; ++e) vr[r][e] = 0.0f;
+                for (int e = 0; e < PL; ++e) vr[r][e] = ((const float *)vp)[e];
             }
         }
     };
-    uint32_t base = lo + wave * kRowsPerWave;
-    load_pass(base, kc, vc);  // in flight while the query heads are prepared
+    const uint32_t base0 = lo + wave * kRowsPerWave;
+    float kc0[KR][KD], vc0[kRowsPerWave][PL], kc1[KR][KD], vc1[kRowsPerWave][PL];
+    __builtin_amdgcn_sched_barrier(0);
+    load_pass(base0, kc0, vc0);
+    load_pass(base0 + kRowsPerPass, kc1, vc1);
+    __builtin_amdgcn_sched_barrier(0);
 
-    const float *cs = a.table + (uint64_t)count * DIM;
-    for (uint32_t g = wave; g < (uint32_t)G; g += kAttnWaves) {
-        const float *x = a.qkv + (uint64_t)(kvh * G + g) * DIM;
-        float inv = head_inverse(x, DIM, lane);
-        for (uint32_t j = lane; j < half; j += 64) {
-            float va = (x[j] * inv) * (bf16f(a.qn[j]) + 1.0f);
-            float vb = (x[j + half] * inv) * (bf16f(a.qn[j + half]) + 1.0f);
-            float c = cs[j], sn = cs[half + j];
-            float p0 = va * c, p1 = vb * sn, p2 = vb * c, p3 = va * sn;
-            qs[g * DIM + j] = p0 - p1;
-            qs[g * DIM + j + half] = p2 + p3;
+    // Offset-1 head RMSNorm then split-half rotation (src/qkv.s:36-67,
+    // tests/rope_reference.s:14-30).
+    if (qwave) {
+        float ss = qx[0] * qx[0];
+        float t = qx[1] * qx[1];
+        ss = wave_sum(ss + t);
+        float ms = ss / (float)DIM;
+        ms = ms + 0.000001f;
+        const float inv = 1.0f / __builtin_sqrtf(ms);
+        if (hl) {
+            float va = (qx[0] * inv) * (qw[0] + 1.0f);
+            float vb = (qx[1] * inv) * (qw[1] + 1.0f);
+            float p0 = va * rc, p1 = vb * rs, p2 = vb * rc, p3 = va * rs;
+            qs[wave * DIM + lane] = p0 - p1;
+            qs[wave * DIM + lane + HALF] = p2 + p3;
         }
     }
-    const bool owner = count >= lo && count < hi;
-    if (owner && wave == kAttnWaves - 1) {
-        const float *x = a.qkv + (uint64_t)(a.qh + kvh) * DIM;
-        const float *vs = a.qkv + (uint64_t)(a.qh + a.kh + kvh) * DIM;
-        float inv = head_inverse(x, DIM, lane);
-        const uint64_t o = (uint64_t)count * width + (uint64_t)kvh * DIM;
-        for (uint32_t j = lane; j < half; j += 64) {
-            float va = (x[j] * inv) * (bf16f(a.kn[j]) + 1.0f);
-            float vb = (x[j + half] * inv) * (bf16f(a.kn[j + half]) + 1.0f);
-            float c = cs[j], sn = cs[half + j];
-            float p0 = va * c, p1 = vb * sn, p2 = vb * c, p3 = va * sn;
+    if (kwave && owner) {
+        float ss = kx[0] * kx[0];
+        float t = kx[1] * kx[1];
+        ss = wave_sum(ss + t);
+        float ms = ss / (float)DIM;
+        ms = ms + 0.000001f;
+        const float inv = 1.0f / __builtin_sqrtf(ms);
+        if (hl) {
+            const uint64_t o = (uint64_t)count * width + (uint64_t)kvh * DIM;
+            float va = (kx[0] * inv) * (kw[0] + 1.0f);
+            float vb = (kx[1] * inv) * (kw[1] + 1.0f);
+            float p0 = va * rc, p1 = vb * rs, p2 = vb * rc, p3 = va * rs;
             float ra = p0 - p1, rb = p2 + p3;
-            float v0 = vs[j], v1 = vs[j + half];
-            knew[j] = ra;
-            knew[j + half] = rb;
-            vnew[j] = v0;
-            vnew[j + half] = v1;
-            a.k_raw[o + j] = va;
-            a.k_raw[o + j + half] = vb;
-            a.k_rot[o + j] = ra;
-            a.k_rot[o + j + half] = rb;
-            a.v[o + j] = v0;
-            a.v[o + j + half] = v1;
+            knew[lane] = ra;
+            knew[lane + HALF] = rb;
+            vnew[lane] = vx[0];
+            vnew[lane + HALF] = vx[1];
+            a.k_raw[o + lane] = va;
+            a.k_raw[o + lane + HALF] = vb;
+            a.k_rot[o + lane] = ra;
+            a.k_rot[o + lane + HALF] = rb;
+            a.v[o + lane] = vx[0];
+            a.v[o + lane + HALF] = vx[1];
             if (a.stage) {
                 float *st = a.stage + (uint64_t)kvh * DIM;
-                st[j] = va;
-                st[j + half] = vb;
-                st[width + j] = v0;
-                st[width + j + half] = v1;
-                st[2 * width + j] = ra;
-                st[2 * width + j + half] = rb;
+                st[lane] = va;
+                st[lane + HALF] = vb;
+                st[width + lane] = vx[0];
+                st[width + lane + HALF] = vx[1];
+                st[2 * width + lane] = ra;
+                st[2 * width + lane + HALF] = rb;
             }
         }
     }
     __syncthreads();
 
-    float q[G][KD];
-#pragma unroll
-    for (int g = 0; g < G; ++g)
-#pragma unroll
-        for (int i = 0; i < KD; ++i) q[g][i] = qs[g * DIM + kd0 + i];
     const float scale = 1.0f / __builtin_sqrtf((float)DIM);
     float m[G], l[G], acc[G][PL];
 #pragma unroll
@@ -896,47 +1026,43 @@ __global__ __launch_bounds__(kAttnThreads) void decode_attention_kernel(DecodeAt
         for (int e = 0; e < PL; ++e) acc[g][e] = 0.0f;
     }
     float *pwave = pw + wave * kRowsPerWave * G;
-    for (; base < hi; base += kRowsPerPass) {
-        const bool more = base + kRowsPerPass < hi;
-        // The appended row comes from LDS (its global copy is being written).
-#pragma unroll
-        for (int j = 0; j < KR; ++j)
-            if (base + rg + 4 * j == count)
-#pragma unroll
-                for (int i = 0; i < KD; ++i) kc[j][i] = knew[kd0 + i];
-#pragma unroll
-        for (int r = 0; r < (int)kRowsPerWave; ++r)
-            if (base + r == count)
-#pragma unroll
-                for (int e = 0; e < PL; ++e) vc[r][e] = vnew[lane + 64 * e];
+    auto consume = [&](uint32_t base, float (&kc)[KR][KD], float (&vc)[kRowsPerWave][PL]) {
 #pragma unroll
         for (int g = 0; g < G; ++g) {
+            // The query slice is read from LDS per pass, not held in registers.
+            float q[KD];
+#pragma unroll
+            for (int i = 0; i < KD; i += 4) {
+                f32x4 x = *(const f32x4 *)(qs + g * DIM + kd0 + i);
+                q[i] = x.x;
+                q[i + 1] = x.y;
+                q[i + 2] = x.z;
+                q[i + 3] = x.w;
+            }
             float sc[KR];
             float mx = -__builtin_inff();
 #pragma unroll
             for (int j = 0; j < KR; ++j) {
                 float s = 0.0f;
 #pragma unroll
-                for (int i = 0; i < KD; ++i) s = __builtin_fmaf(q[g][i], kc[j][i], s);
-#pragma unroll
-                for (int o = 1; o < 16; o <<= 1) s = s + __shfl_xor(s, o, 64);
-                const bool valid = base + rg + 4 * j < hi;
+                for (int i = 0; i < KD; ++i) s = __builtin_fmaf(q[i], kc[j][i], s);
+                s = row_sum16(s);
+                const bool valid = base + rg + 4 * j < hr;
                 sc[j] = valid ? s * scale : -__builtin_inff();
                 mx = fmaxf(mx, sc[j]);
             }
-            mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-            mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+            mx = rows_max(mx);
             const float mn = fmaxf(m[g], mx);
             const float corr = plamo_exp(m[g] - mn);
             float ps = 0.0f;
 #pragma unroll
             for (int j = 0; j < KR; ++j) {
-                float p = sc[j] == -__builtin_inff() ? 0.0f : plamo_exp(sc[j] - mn);
+                // Masked rows: exp(-inf) is 0 (plamo_exp maps NaN and -inf to 0).
+                float p = plamo_exp(sc[j] - mn);
                 ps += p;
                 if ((lane & 15) == 0) pwave[(rg + 4 * j) * G + g] = p;
             }
-            ps = ps + __shfl_xor(ps, 16, 64);
-            ps = ps + __shfl_xor(ps, 32, 64);
+            ps = rows_sum(ps);
             l[g] = l[g] * corr + ps;
             m[g] = mn;
 #pragma unroll
@@ -955,7 +1081,19 @@ __global__ __launch_bounds__(kAttnThreads) void decode_attention_kernel(DecodeAt
             }
         }
         __builtin_amdgcn_wave_barrier();
-        if (more) load_pass(base + kRowsPerPass, kc, vc);
+    };
+    // The scheduling fences keep each refill after the consumption of the
+    // buffer it overwrites (otherwise the scheduler hoists it and spills).
+    for (uint32_t b = base0; b < hr; b += 2 * kRowsPerPass) {
+        consume(b, kc0, vc0);
+        __builtin_amdgcn_sched_barrier(0);
+        load_pass(b + 2 * kRowsPerPass, kc0, vc0);
+        __builtin_amdgcn_sched_barrier(0);
+        if (b + kRowsPerPass >= hr) break;
+        consume(b + kRowsPerPass, kc1, vc1);
+        __builtin_amdgcn_sched_barrier(0);
+        load_pass(b + 3 * kRowsPerPass, kc1, vc1);
+        __builtin_amdgcn_sched_barrier(0);
     }
     // Merge the waves in LDS.
 #pragma unroll
@@ -966,17 +1104,34 @@ __global__ __launch_bounds__(kAttnThreads) void decode_attention_kernel(DecodeAt
             wp[1] = l[g];
         }
 #pragma unroll
-        for (int e = 0; e < PL; ++e) wp[2 + lane + 64 * e] = acc[g][e];
+        for (int e = 0; e < PL; ++e) wp[2 + lane * PL + e] = acc[g][e];
+    }
+    // The appended row as a partial of its own: max = its score, sum = 1,
+    // accumulator = its value row.
+    if (kwave && owner) {
+        for (int g = 0; g < G; ++g) {
+            float s = 0.0f;
+#pragma unroll
+            for (int e = 0; e < PL; ++e)
+                s = __builtin_fmaf(qs[g * DIM + lane * PL + e], knew[lane * PL + e], s);
+            s = wave_sum(s);
+            float *wp = wpart + (kAttnWaves * G + g) * rec;
+            if (lane == 0) {
+                wp[0] = s * scale;
+                wp[1] = 1.0f;
+            }
+#pragma unroll
+            for (int e = 0; e < PL; ++e) wp[2 + lane * PL + e] = vnew[lane * PL + e];
+        }
     }
     __syncthreads();
+    const uint32_t parts = kAttnWaves + (owner ? 1 : 0);
     for (uint32_t i = threadIdx.x; i < G * DIM; i += kAttnThreads) {
         const uint32_t g = i / DIM, d = i % DIM;
         float mx = -__builtin_inff();
-#pragma unroll
-        for (uint32_t w = 0; w < kAttnWaves; ++w) mx = fmaxf(mx, wpart[(w * G + g) * rec]);
+        for (uint32_t w = 0; w < parts; ++w) mx = fmaxf(mx, wpart[(w * G + g) * rec]);
         float sum = 0.0f, o = 0.0f;
-#pragma unroll
-        for (uint32_t w = 0; w < kAttnWaves; ++w) {
+        for (uint32_t w = 0; w < parts; ++w) {
             const float *wp = wpart + (w * G + g) * rec;
             const float f = wp[0] == -__builtin_inff() ? 0.0f : plamo_exp(wp[0] - mx);
             sum = __builtin_fmaf(wp[1], f, sum);
@@ -1042,7 +1197,8 @@ bool decode_attention_supported(uint32_t dim, uint32_t group) {
 
 static size_t decode_attention_lds(uint32_t dim, uint32_t group) {
     const uint32_t rows = group <= 4 ? 16 : 8;
-    return (group * dim + 2 * dim + kAttnWaves * rows * group + kAttnWaves * group * (dim + 2)) *
+    return (group * dim + 2 * dim + kAttnWaves * rows * group +
+            (kAttnWaves + 1) * group * (dim + 2)) *
            sizeof(float);
 }
 

@@ -106,3 +106,15 @@ def test_c2_greedy_64_steps():
         gpu.close()
         cpu.close()
         syn.close()
+
+
+def test_long_context_split_attention():
+    # Contexts past 1024 rows split a KV head over several blocks whose
+    # partials are merged by the last one; 1023 -> 1025 crosses the boundary.
+    syn = plamo_hip.Synthetic(512, 2, 8, 2, 128, 1024, 500, window=4096, global_capacity=8192,
+                              pattern=2, embedding_std=1.0, seed=404)
+    try:
+        run_pair(syn, steps=3, prompt=None, fill=1023)
+        run_pair(syn, steps=3, prompt=None, fill=3000)
+    finally:
+        syn.close()
