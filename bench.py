@@ -102,6 +102,42 @@ def cpu_baseline(inst: plamo_hip.Instance, token: int, seconds: float, cfg: dict
                       f"{elapsed:.1f} s"}
 
 
+def copy_calibration(nbytes: int, reps: int = 5):
+    """Device-to-device copies of a known size through the HIP runtime the
+    library links (reads nbytes, writes nbytes per dispatch)."""
+    hip = ctypes.CDLL("libamdhip64.so.7")  # the soname libplamo_hip.so links
+    src, dst = ctypes.c_void_p(), ctypes.c_void_p()
+    if hip.hipMalloc(ctypes.byref(src), ctypes.c_size_t(nbytes)) or \
+            hip.hipMalloc(ctypes.byref(dst), ctypes.c_size_t(nbytes)):
+        raise RuntimeError("hipMalloc failed")
+    try:
+        hip.hipMemset(src, 0, ctypes.c_size_t(nbytes))
+        hip.hipDeviceSynchronize()
+        start = time.perf_counter()
+        for _ in range(reps):
+            if hip.hipMemcpy(dst, src, ctypes.c_size_t(nbytes), 3):  # hipMemcpyDeviceToDevice
+                raise RuntimeError("hipMemcpy failed")
+        hip.hipDeviceSynchronize()
+        elapsed = time.perf_counter() - start
+        log(f"copy calibration: {reps} x {nbytes >> 20} MiB device copies, "
+            f"{2 * nbytes * reps / elapsed / 1e9:.0f} GB/s read+write (host-timed)")
+    finally:
+        hip.hipFree(src)
+        hip.hipFree(dst)
+
+
+def measured_traffic():
+    """HBM bytes per launch of the gate/up GEMV from the committed rocprofv3
+    FETCH_SIZE / WRITE_SIZE summary (copy-calibrated), or None."""
+    path = ROOT / "profiles" / "gate_up_gemv_c4_hbm_traffic.md"
+    if not path.exists():
+        return None
+    for line in path.read_text().splitlines():
+        if line.startswith("traffic_bytes_per_launch:"):
+            return int(line.split(":", 1)[1].strip())
+    return None
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -111,6 +147,12 @@ def main() -> int:
     ap.add_argument("--prompt", type=int, default=128)
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--ttft-sizes", default="81,128,455",
+                    help="comma-separated prompt lengths for TTFT ('' skips)")
+    ap.add_argument("--kernel-reps", type=int, default=50)
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="also run device-to-device copies of MIB MiB (the known-size "
+                         "kernel that scales rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path "
@@ -138,7 +180,7 @@ def main() -> int:
 
     # TTFT: restore the prefix snapshot, prefill the body, logits on the host.
     ttft = {}
-    for n in (81, 128, 455):
+    for n in [int(x) for x in args.ttft_sizes.split(",") if x]:
         times = []
         for _ in range(4):
             start = time.perf_counter()
@@ -180,13 +222,16 @@ def main() -> int:
              plamo_hip.KERNEL_GATE_UP: "gate_up_swiglu_gemv", plamo_hip.KERNEL_DOWN: "down_gemv",
              plamo_hip.KERNEL_HEAD: "head_gemv", plamo_hip.KERNEL_ATTENTION: "decode_attention"}
     for which, name in names.items():
-        ms, nbytes = be.time_kernel(inst, 0, which, 50)
+        ms, nbytes = be.time_kernel(inst, 0, which, args.kernel_reps)
         kernels[name] = {"us": round(ms * 1e3, 2), "bytes": int(nbytes),
                          "GBps": round(nbytes / ms / 1e6, 1)}
         log(f"kernel {name}: {ms * 1e3:.2f} us, {nbytes / ms / 1e6:.0f} GB/s")
     dom = kernels["gate_up_swiglu_gemv"]
 
+    if args.copy_calibration:
+        copy_calibration(args.copy_calibration << 20)
     ttft_flop = prefill_flop(plamo_hip.CONFIGS[args.config], PREFIX, 128 - PREFIX)
+    traffic = measured_traffic()
     result = {
         "metric": "decode tok/s + % HBM roofline (8B-class, bs=1); prefill TTFT @128 tok",
         "value": round(args.steps / elapsed, 2),
@@ -211,14 +256,15 @@ def main() -> int:
                               "frac": round(step_bytes / ms_step / 1e6 / HBM_PEAK_GBPS, 4),
                               "gpu_ms_per_step": round(gpu_ms_step, 4)},
         "ttft_ms": {str(k): round(v, 3) for k, v in ttft.items()},
-        "prefill_roofline_128": {"flop": ttft_flop,
-                                 "achieved_TFLOPs": round(ttft_flop / ttft[128] / 1e9, 2),
-                                 "peak_TFLOPs": FP32_MFMA_PEAK_TFLOPS,
-                                 "frac": round(ttft_flop / ttft[128] / 1e9 / FP32_MFMA_PEAK_TFLOPS,
-                                               4)},
+        "prefill_roofline_128": ({"flop": ttft_flop,
+                                  "achieved_TFLOPs": round(ttft_flop / ttft[128] / 1e9, 2),
+                                  "peak_TFLOPs": FP32_MFMA_PEAK_TFLOPS,
+                                  "frac": round(ttft_flop / ttft[128] / 1e9 /
+                                                FP32_MFMA_PEAK_TFLOPS, 4)}
+                                 if 128 in ttft else None),
         "roofline": {"bound": "hbm", "kernel": "gemv_kernel<VEC,SWIGLU> (gate/up + SwiGLU)",
                      "achieved": dom["GBps"], "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": round(dom["GBps"] / HBM_PEAK_GBPS, 4), "traffic": None},
+                     "frac": round(dom["GBps"] / HBM_PEAK_GBPS, 4), "traffic": traffic},
         "kernels": kernels,
     }
     if not args.no_cpu:
