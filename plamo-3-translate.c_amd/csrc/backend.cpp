@@ -117,6 +117,7 @@ struct plamo_metal {
     uint64_t verification_tokens = 0, verification_index = 0;
 
     Buffer lin_in, lin_out, mlp_state, mlp_norm, mlp_gu, mlp_act, mlp_branch, mlp_norms;
+    GemmWorkspace gemm{};  // split-K partial tiles and arrival counters
 
     hipGraphExec_t graph = nullptr;
     uint64_t epoch = 1, graph_epoch = 0;
@@ -742,6 +743,23 @@ int ensure_prompt(plamo_metal *m, struct model *model, uint64_t rows) {
     return 1;
 }
 
+// Split-K scratch of the prompt GEMMs, allocated once; the counters start at
+// zero and every GEMM leaves them zero.
+const GemmWorkspace *gemm_workspace(plamo_metal *m) {
+    if (m->gemm.partial) return &m->gemm;
+    float *partial = dev_alloc<float>(m, kGemmPartialFloats);
+    uint32_t *counters = dev_alloc<uint32_t>(m, kGemmCounters);
+    if (!partial || !counters || hipMemset(counters, 0, kGemmCounters * 4) != hipSuccess) {
+        (void)hipGetLastError();
+        dev_free(m, partial);
+        dev_free(m, counters);
+        problem(m, "cannot allocate GEMM scratch");
+        return nullptr;
+    }
+    m->gemm = GemmWorkspace{partial, kGemmPartialFloats, counters, kGemmCounters};
+    return &m->gemm;
+}
+
 int ensure_window_scratch(plamo_metal *m, struct model *model) {
     uint64_t need = 0;
     for (uint64_t i = 0; i < model->count; ++i)
@@ -1032,6 +1050,8 @@ int run_prompt(plamo_metal *m, struct model *model, const uint32_t *ids, uint64_
     std::vector<char> stale;
     if (!sync_from_host(m, model, stale)) return -1;
     if (!ensure_prompt(m, model, T) || !ensure_window_scratch(m, model)) return -1;
+    const GemmWorkspace *ws = gemm_workspace(m);
+    if (!ws) return -1;
     if (verify) {
         uint64_t prop = L * 3 * kMaxVerify * m->max_width;
         if (!m->v_state) {
@@ -1085,7 +1105,7 @@ int run_prompt(plamo_metal *m, struct model *model, const uint32_t *ids, uint64_
         const RopeTable &rope = m->ropes[d.rope];
         const uint64_t qkv_w = (uint64_t)(d.qh + 2 * d.kh) * d.dim, aw = (uint64_t)d.qh * d.dim;
         HIP_FAIL(m, launch_norm_rows(s, state, h, pre, 1.0f, norm, h, h, T));
-        HIP_FAIL(m, launch_gemm(s, norm, h, d.qkv, qkv_w, h, T, qkv, qkv_w));
+        HIP_FAIL(m, launch_gemm(s, norm, h, d.qkv, qkv_w, h, T, qkv, qkv_w, ws));
         n += 2;
         if (stale[i] && (verify || !overflow[i])) {
             HIP_FAIL(m, launch_rerotate(s, d.k, d.rot, rope.table, c->count, d.kh, d.dim));
@@ -1188,20 +1208,20 @@ int run_prompt(plamo_metal *m, struct model *model, const uint32_t *ids, uint64_
             HIP_FAIL(m, launch_residual_rows(s, st, branch, mpost, kMlpOffset, h, 1));
             n += 5;
         } else {
-            HIP_FAIL(m, launch_gemm(s, attn + first * aw, aw, d.o, h, aw, rows, branch, h));
+            HIP_FAIL(m, launch_gemm(s, attn + first * aw, aw, d.o, h, aw, rows, branch, h, ws));
             HIP_FAIL(m, launch_residual_rows(s, st, branch, post, kAttentionOffset, h, rows));
             HIP_FAIL(m, launch_norm_rows(s, st, h, mpre, 1.0f, norm, h, h, rows));
             HIP_FAIL(m, launch_gemm(s, norm, h, d.gu, 2 * (uint64_t)d.inter, h, rows, gu,
-                                   2 * (uint64_t)d.inter));
+                                   2 * (uint64_t)d.inter, ws));
             HIP_FAIL(m, launch_swiglu_rows(s, gu, act, d.inter, rows));
-            HIP_FAIL(m, launch_gemm(s, act, d.inter, d.down, h, d.inter, rows, branch, h));
+            HIP_FAIL(m, launch_gemm(s, act, d.inter, d.down, h, d.inter, rows, branch, h, ws));
             HIP_FAIL(m, launch_residual_rows(s, st, branch, mpost, kMlpOffset, h, rows));
             n += 7;
         }
     }
     if (verify) {
         HIP_FAIL(m, launch_norm_rows(s, state, h, m->final_norm, 1.0f, m->v_norm, h, h, T));
-        HIP_FAIL(m, launch_gemm(s, m->v_norm, h, m->head, V, h, T, m->v_logits, V));
+        HIP_FAIL(m, launch_gemm(s, m->v_norm, h, m->head, V, h, T, m->v_logits, V, ws));
         HIP_FAIL(m, launch_argmax_rows(s, m->v_logits, V, T, m->v_next));
         HIP_FAIL(m, hipMemcpyAsync(m->v_state, state, T * h * 4, hipMemcpyDeviceToDevice, s));
         HIP_FAIL(m, hipMemcpyAsync(m->v_host, m->v_state, T * h * 4, hipMemcpyDeviceToHost, s));
@@ -1400,7 +1420,9 @@ int plamo_metal_linear(struct plamo_metal *m, const struct plamo_matmul *mm) {
         p.src = as<float>(in);
         ok = launch_gemv(m->stream, w, N, K, p, as<float>(out), 0, 2 * m->cus) == hipSuccess;
     } else if (ok) {
-        ok = launch_gemm(m->stream, as<float>(in), K, w, N, K, T, as<float>(out), N) == hipSuccess;
+        const GemmWorkspace *ws = gemm_workspace(m);
+        ok = ws && launch_gemm(m->stream, as<float>(in), K, w, N, K, T, as<float>(out), N, ws) ==
+                       hipSuccess;
     }
     ok = ok && hipMemcpy2DAsync(mm->output, mm->output_stride * 4, out.ptr, N * 4, N * 4, T,
                                 hipMemcpyDeviceToHost, m->stream) == hipSuccess;
@@ -1425,8 +1447,10 @@ int plamo_metal_mlp(struct plamo_metal *m, const struct mlp *mlp, float *states,
     }
     Buffer &st = m->mlp_state, &nrm = m->mlp_norm, &g = m->mlp_gu, &a = m->mlp_act,
            &b = m->mlp_branch, &norms = m->mlp_norms;
-    bool ok = ensure(m, st, T * h * 4) && ensure(m, nrm, T * h * 4) && ensure(m, g, T * 2 * I * 4) &&
-              ensure(m, a, T * I * 4) && ensure(m, b, T * h * 4) && ensure(m, norms, 2 * h * 2);
+    const GemmWorkspace *ws = gemm_workspace(m);
+    bool ok = ws && ensure(m, st, T * h * 4) && ensure(m, nrm, T * h * 4) &&
+              ensure(m, g, T * 2 * I * 4) && ensure(m, a, T * I * 4) && ensure(m, b, T * h * 4) &&
+              ensure(m, norms, 2 * h * 2);
     hipStream_t s = m->stream;
     ok = ok && hipMemcpyAsync(norms.ptr, mlp->pre, h * 2, hipMemcpyHostToDevice, s) == hipSuccess &&
          hipMemcpyAsync(as<uint16_t>(norms) + h, mlp->post, h * 2, hipMemcpyHostToDevice, s) ==
@@ -1434,9 +1458,9 @@ int plamo_metal_mlp(struct plamo_metal *m, const struct mlp *mlp, float *states,
          hipMemcpyAsync(st.ptr, states, T * h * 4, hipMemcpyHostToDevice, s) == hipSuccess;
     if (ok) begin_timing(m);
     ok = ok && launch_norm_rows(s, as<float>(st), h, as<uint16_t>(norms), 1.0f, as<float>(nrm), h, h, T) == hipSuccess &&
-         launch_gemm(s, as<float>(nrm), h, gu, 2 * I, h, T, as<float>(g), 2 * I) == hipSuccess &&
+         launch_gemm(s, as<float>(nrm), h, gu, 2 * I, h, T, as<float>(g), 2 * I, ws) == hipSuccess &&
          launch_swiglu_rows(s, as<float>(g), as<float>(a), I, T) == hipSuccess &&
-         launch_gemm(s, as<float>(a), I, down, h, I, T, as<float>(b), h) == hipSuccess &&
+         launch_gemm(s, as<float>(a), I, down, h, I, T, as<float>(b), h, ws) == hipSuccess &&
          launch_residual_rows(s, as<float>(st), as<float>(b), as<uint16_t>(norms) + h, kMlpOffset, h, T) == hipSuccess &&
          hipMemcpyAsync(states, st.ptr, T * h * 4, hipMemcpyDeviceToHost, s) == hipSuccess &&
          end_timing(m);

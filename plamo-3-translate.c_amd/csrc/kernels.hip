@@ -689,10 +689,256 @@ static hipError_t gemm_variant(hipStream_t stream, const float *x, uint64_t x_st
     return hipGetLastError();
 }
 
+// ---------------------------------------------------------------- split-BF16 MFMA GEMM
+// C[t, r] = sum_k X[t, k] * W[r, k] with FP32 X and BF16 W on the BF16 matrix
+// cores, exactly: each FP32 x is split into three BF16 terms
+// x = hi + mid + lo (hi = x truncated to 8 significant bits, mid = the next 8
+// of the remainder, lo = the rest, which has at most 8 significant bits), so
+// the split loses nothing, every product W * term is exact in FP32, and the
+// three products accumulate in FP32 (v_mfma_f32_32x32x16_bf16). Weights are
+// used as stored, with no widening.
+//
+// Block: 4 waves as 2 x 2, each wave WM x WN tiles of 32 x 32, so the block
+// covers BM = 64 WM token rows by BN = 64 WN weight rows. K advances 64 per
+// stage: the block loads the next stage (X as FP32, W as BF16) into registers
+// while the matrix cores run on the current one, then splits X into its three
+// planes and stores both into the other LDS buffer (one barrier per stage).
+// Grid: (N tiles, M tiles, K splits); with several K splits each block writes
+// its partial tile and the last block of a tile sums them in split order.
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+constexpr int kSplitBK = 64;
+constexpr int kSplitPitch = kSplitBK + 8;  // BF16 per LDS row: +16 bytes keeps ds_read_b128 conflict-free
+
+__device__ __forceinline__ uint32_t pack_hi16(uint32_t a, uint32_t b) {
+    return (b & 0xffff0000u) | (a >> 16);
+}
+
+template <int WM, int WN>
+__global__ __launch_bounds__(256) void gemm_split_kernel(GemmSplit g) {
+    constexpr int BM = 64 * WM, BN = 64 * WN;
+    constexpr int FX = BM / 4;        // X floats staged per thread per stage
+    constexpr int TX = kSplitBK / FX; // threads per X row
+    constexpr int FW = BN / 4;        // W BF16 staged per thread per stage
+    constexpr int TW = kSplitBK / FW; // threads per W row
+    constexpr int BUF = (3 * BM + BN) * kSplitPitch;  // BF16 per LDS buffer
+    extern __shared__ uint16_t lds[];
+    __shared__ int is_last;
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t wm = wave >> 1, wn = wave & 1;
+    const uint32_t m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+    const uint32_t kper = g.k / g.splits;
+    const uint32_t kbeg = blockIdx.z * kper, kend = kbeg + kper;
+
+    // Staging assignment (clamped rows: rows past T or N load a valid row whose
+    // results are never stored).
+    const uint32_t xr = threadIdx.x / TX, xc = (threadIdx.x % TX) * FX;
+    const uint32_t wr = threadIdx.x / TW, wc = (threadIdx.x % TW) * FW;
+    const float *xsrc = g.x + (uint64_t)min(m0 + xr, g.t - 1) * g.ldx + xc;
+    const uint16_t *wsrc = g.w + (uint64_t)min(n0 + wr, g.n - 1) * g.k + wc;
+    const bool xvalid = m0 + xr < g.t;
+    f32x4 xv[FX / 4];
+    u32x4 wv[FW / 8];
+    auto load = [&](uint32_t k) {
+#pragma unroll
+        for (int i = 0; i < FX / 4; ++i) xv[i] = *(const f32x4 *)(xsrc + k + 4 * i);
+#pragma unroll
+        for (int i = 0; i < FW / 8; ++i)
+            wv[i] = __builtin_nontemporal_load((const u32x4 *)(wsrc + k) + i);
+    };
+    auto store = [&](int buf) {
+        uint16_t *xl = lds + buf * BUF;
+        uint16_t *wl = xl + 3 * BM * kSplitPitch;
+#pragma unroll
+        for (int i = 0; i < FX / 8; ++i) {
+            uint32_t h[8], md[8], lo[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const f32x4 q = xv[2 * i + e / 4];
+                float x = e % 4 == 0 ? q.x : e % 4 == 1 ? q.y : e % 4 == 2 ? q.z : q.w;
+                x = xvalid ? x : 0.0f;
+                const uint32_t u = __float_as_uint(x);
+                h[e] = u & 0xffff0000u;
+                const float r = x - __uint_as_float(h[e]);
+                md[e] = __float_as_uint(r) & 0xffff0000u;
+                lo[e] = __float_as_uint(r - __uint_as_float(md[e]));
+            }
+            const uint32_t col = xc + 8 * i;
+            u32x4 ph = {pack_hi16(h[0], h[1]), pack_hi16(h[2], h[3]), pack_hi16(h[4], h[5]),
+                        pack_hi16(h[6], h[7])};
+            u32x4 pm = {pack_hi16(md[0], md[1]), pack_hi16(md[2], md[3]),
+                        pack_hi16(md[4], md[5]), pack_hi16(md[6], md[7])};
+            u32x4 pl = {pack_hi16(lo[0], lo[1]), pack_hi16(lo[2], lo[3]),
+                        pack_hi16(lo[4], lo[5]), pack_hi16(lo[6], lo[7])};
+            *(u32x4 *)(xl + (0 * BM + xr) * kSplitPitch + col) = ph;
+            *(u32x4 *)(xl + (1 * BM + xr) * kSplitPitch + col) = pm;
+            *(u32x4 *)(xl + (2 * BM + xr) * kSplitPitch + col) = pl;
+        }
+#pragma unroll
+        for (int i = 0; i < FW / 8; ++i) *(u32x4 *)(wl + wr * kSplitPitch + wc + 8 * i) = wv[i];
+    };
+
+    f32x16 acc[WM][WN];
+#pragma unroll
+    for (int i = 0; i < WM; ++i)
+#pragma unroll
+        for (int j = 0; j < WN; ++j)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
+
+    load(kbeg);
+    store(0);
+    __syncthreads();
+    int buf = 0;
+    for (uint32_t k = kbeg; k < kend; k += kSplitBK) {
+        // Next stage (clamped to the last one: unconditional, so the compiler
+        // keeps exact wait counts).
+        load(min(k + kSplitBK, kend - kSplitBK));
+        const uint16_t *xl = lds + buf * BUF;
+        const uint16_t *wl = xl + 3 * BM * kSplitPitch;
+#pragma unroll
+        for (int ks = 0; ks < kSplitBK / 16; ++ks) {
+            const uint32_t kk = ks * 16 + 8 * (lane >> 5);
+            bf16x8 a[3][WM], b[WN];
+#pragma unroll
+            for (int i = 0; i < WM; ++i) {
+                const uint32_t row = wm * 32 * WM + 32 * i + (lane & 31);
+#pragma unroll
+                for (int p = 0; p < 3; ++p)
+                    a[p][i] = *(const bf16x8 *)(xl + (p * BM + row) * kSplitPitch + kk);
+            }
+#pragma unroll
+            for (int j = 0; j < WN; ++j) {
+                const uint32_t row = wn * 32 * WN + 32 * j + (lane & 31);
+                b[j] = *(const bf16x8 *)(wl + row * kSplitPitch + kk);
+            }
+#pragma unroll
+            for (int p = 0; p < 3; ++p)
+#pragma unroll
+                for (int i = 0; i < WM; ++i)
+#pragma unroll
+                    for (int j = 0; j < WN; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[p][i], b[j],
+                                                                             acc[i][j], 0, 0, 0);
+        }
+        if (k + kSplitBK < kend) store(buf ^ 1);
+        __syncthreads();
+        buf ^= 1;
+    }
+
+    // D layout of v_mfma_f32_32x32x16: value v of lane l is row
+    // 8 (v / 4) + 4 (l / 32) + v % 4, column l % 32 of the 32 x 32 tile.
+    const uint32_t tile = blockIdx.y * gridDim.x + blockIdx.x;
+    const uint32_t tiles = gridDim.x * gridDim.y;
+    if (g.splits == 1) {
+#pragma unroll
+        for (int i = 0; i < WM; ++i)
+#pragma unroll
+            for (int j = 0; j < WN; ++j) {
+                const uint32_t col = n0 + wn * 32 * WN + 32 * j + (lane & 31);
+#pragma unroll
+                for (int v = 0; v < 16; ++v) {
+                    const uint32_t row =
+                        m0 + wm * 32 * WM + 32 * i + 8 * (v / 4) + 4 * (lane >> 5) + v % 4;
+                    if (row < g.t && col < g.n) g.y[(uint64_t)row * g.ldy + col] = acc[i][j][v];
+                }
+            }
+        return;
+    }
+    // Partial tile, laid out [split][tile][wave][i][j][v][lane] (coalesced).
+    float *part = g.partial + ((uint64_t)blockIdx.z * tiles + tile) * (BM * BN);
+#pragma unroll
+    for (int i = 0; i < WM; ++i)
+#pragma unroll
+        for (int j = 0; j < WN; ++j)
+#pragma unroll
+            for (int v = 0; v < 16; ++v)
+                part[(((wave * WM + i) * WN + j) * 16 + v) * 64 + lane] = acc[i][j][v];
+    __threadfence();
+    __syncthreads();
+    if (threadIdx.x == 0) is_last = atomicAdd(&g.counters[tile], 1u) + 1 == g.splits;
+    __syncthreads();
+    if (!is_last) return;
+    __threadfence();
+#pragma unroll
+    for (int i = 0; i < WM; ++i)
+#pragma unroll
+        for (int j = 0; j < WN; ++j)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                const uint64_t at = (((wave * WM + i) * WN + j) * 16 + v) * 64 + lane;
+                float sum = g.partial[(uint64_t)tile * (BM * BN) + at];
+                for (uint32_t sp = 1; sp < g.splits; ++sp)
+                    sum = sum + g.partial[((uint64_t)sp * tiles + tile) * (BM * BN) + at];
+                acc[i][j][v] = sum;
+            }
+#pragma unroll
+    for (int i = 0; i < WM; ++i)
+#pragma unroll
+        for (int j = 0; j < WN; ++j) {
+            const uint32_t col = n0 + wn * 32 * WN + 32 * j + (lane & 31);
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                const uint32_t row =
+                    m0 + wm * 32 * WM + 32 * i + 8 * (v / 4) + 4 * (lane >> 5) + v % 4;
+                if (row < g.t && col < g.n) g.y[(uint64_t)row * g.ldy + col] = acc[i][j][v];
+            }
+        }
+    if (threadIdx.x == 0) g.counters[tile] = 0;
+}
+
+template <int WM, int WN>
+static hipError_t gemm_split_variant(hipStream_t stream, GemmSplit g, const GemmWorkspace &ws) {
+    constexpr uint32_t BM = 64 * WM, BN = 64 * WN;
+    const uint32_t nt = (g.n + BN - 1) / BN, mt = (g.t + BM - 1) / BM;
+    const uint32_t tiles = nt * mt, kblocks = g.k / kSplitBK;
+    // Enough blocks for the 256 CUs, each split at least two stages long.
+    uint32_t splits = 1;
+    while (tiles * splits < 256 && kblocks % (2 * splits) == 0 && kblocks / (2 * splits) >= 2 &&
+           splits < 16)
+        splits *= 2;
+    if (splits > 1 && ((uint64_t)splits * tiles * BM * BN > ws.partial_floats ||
+                       tiles > ws.counters))
+        splits = 1;
+    g.splits = splits;
+    g.partial = ws.partial;
+    g.counters = ws.counter_base;
+    const size_t lds = 2 * (size_t)(3 * BM + BN) * kSplitPitch * sizeof(uint16_t);
+    static bool attr = false;
+    if (!attr) {
+        hipError_t e = hipFuncSetAttribute((const void *)gemm_split_kernel<WM, WN>,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) return e;
+        attr = true;
+    }
+    gemm_split_kernel<WM, WN><<<dim3(nt, mt, splits), 256, lds, stream>>>(g);
+    return hipGetLastError();
+}
+
+bool gemm_split_supported(const float *x, uint64_t x_stride, const uint16_t *w, uint64_t cols) {
+    return cols % kSplitBK == 0 && x_stride % 4 == 0 && !((uintptr_t)x & 15) &&
+           !((uintptr_t)w & 15) && cols <= (1u << 30);
+}
+
 hipError_t launch_gemm(hipStream_t stream, const float *x, uint64_t x_stride, const uint16_t *w,
                        uint64_t rows, uint64_t cols, uint64_t tokens, float *y,
-                       uint64_t y_stride) {
+                       uint64_t y_stride, const GemmWorkspace *ws) {
     if (!tokens || !rows) return hipSuccess;
+    if (ws && tokens > 1 && rows < (1u << 31) && tokens < (1u << 31) &&
+        gemm_split_supported(x, x_stride, w, cols)) {
+        GemmSplit g{};
+        g.x = x;
+        g.ldx = x_stride;
+        g.w = w;
+        g.n = (uint32_t)rows;
+        g.k = (uint32_t)cols;
+        g.t = (uint32_t)tokens;
+        g.y = y;
+        g.ldy = y_stride;
+        if (tokens <= 64) return gemm_split_variant<1, 2>(stream, g, *ws);
+        return gemm_split_variant<2, 2>(stream, g, *ws);
+    }
     if (tokens <= 16) return gemm_variant<16, 64>(stream, x, x_stride, w, rows, cols, tokens, y, y_stride);
     return gemm_variant<64, 64>(stream, x, x_stride, w, rows, cols, tokens, y, y_stride);
 }
