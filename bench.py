@@ -36,6 +36,9 @@ import plamo_hip  # noqa: E402
 
 HBM_PEAK_GBPS = 8000.0        # MI355X HBM3E
 FP32_MFMA_PEAK_TFLOPS = 157.3  # MI355X dense FP32 matrix
+# The prompt GEMM runs exact FP32 products as three BF16 passes on the
+# 2.5 PFLOP/s BF16 matrix cores: its own ceiling is a third of that.
+SPLIT_BF16_CEILING_TFLOPS = round(2500.0 / 3, 1)
 PREFIX = 12                   # fixed translation-template prefix (runtime/engine.c:358-381)
 
 
@@ -260,7 +263,10 @@ def main() -> int:
                                   "achieved_TFLOPs": round(ttft_flop / ttft[128] / 1e9, 2),
                                   "peak_TFLOPs": FP32_MFMA_PEAK_TFLOPS,
                                   "frac": round(ttft_flop / ttft[128] / 1e9 /
-                                                FP32_MFMA_PEAK_TFLOPS, 4)}
+                                                FP32_MFMA_PEAK_TFLOPS, 4),
+                                  "split_bf16_ceiling_TFLOPs": SPLIT_BF16_CEILING_TFLOPS,
+                                  "frac_of_split_bf16": round(ttft_flop / ttft[128] / 1e9 /
+                                                              SPLIT_BF16_CEILING_TFLOPS, 4)}
                                  if 128 in ttft else None),
         "roofline": {"bound": "hbm", "kernel": "gemv_kernel<VEC,SWIGLU> (gate/up + SwiGLU)",
                      "achieved": dom["GBps"], "peak": HBM_PEAK_GBPS, "unit": "GB/s",

@@ -743,20 +743,32 @@ int ensure_prompt(plamo_metal *m, struct model *model, uint64_t rows) {
     return 1;
 }
 
-// Split-K scratch of the prompt GEMMs, allocated once; the counters start at
-// zero and every GEMM leaves them zero.
-const GemmWorkspace *gemm_workspace(plamo_metal *m) {
-    if (m->gemm.partial) return &m->gemm;
-    float *partial = dev_alloc<float>(m, kGemmPartialFloats);
-    uint32_t *counters = dev_alloc<uint32_t>(m, kGemmCounters);
-    if (!partial || !counters || hipMemset(counters, 0, kGemmCounters * 4) != hipSuccess) {
-        (void)hipGetLastError();
-        dev_free(m, partial);
-        dev_free(m, counters);
-        problem(m, "cannot allocate GEMM scratch");
-        return nullptr;
+// Scratch of the prompt GEMMs for up to `tokens` rows of `cols` columns: the
+// split-K partials and counters are allocated once (the counters start at
+// zero and every GEMM leaves them zero), the BF16 planes of X grow on demand.
+const GemmWorkspace *gemm_workspace(plamo_metal *m, uint64_t tokens, uint64_t cols) {
+    if (!m->gemm.partial) {
+        float *partial = dev_alloc<float>(m, kGemmPartialFloats);
+        uint32_t *counters = dev_alloc<uint32_t>(m, kGemmCounters);
+        if (!partial || !counters || hipMemset(counters, 0, kGemmCounters * 4) != hipSuccess) {
+            (void)hipGetLastError();
+            dev_free(m, partial);
+            dev_free(m, counters);
+            problem(m, "cannot allocate GEMM scratch");
+            return nullptr;
+        }
+        m->gemm.partial = partial;
+        m->gemm.partial_floats = kGemmPartialFloats;
+        m->gemm.counter_base = counters;
+        m->gemm.counters = kGemmCounters;
     }
-    m->gemm = GemmWorkspace{partial, kGemmPartialFloats, counters, kGemmCounters};
+    const uint64_t need = gemm_plane_elems(std::max<uint64_t>(tokens, 128), cols);
+    if (need > m->gemm.plane_elems) {
+        dev_free(m, m->gemm.planes);
+        m->gemm.planes = dev_alloc<uint16_t>(m, need);
+        m->gemm.plane_elems = m->gemm.planes ? need : 0;
+        if (!m->gemm.planes) return nullptr;
+    }
     return &m->gemm;
 }
 
@@ -1050,7 +1062,8 @@ int run_prompt(plamo_metal *m, struct model *model, const uint32_t *ids, uint64_
     std::vector<char> stale;
     if (!sync_from_host(m, model, stale)) return -1;
     if (!ensure_prompt(m, model, T) || !ensure_window_scratch(m, model)) return -1;
-    const GemmWorkspace *ws = gemm_workspace(m);
+    const GemmWorkspace *ws =
+        gemm_workspace(m, T, std::max({h, m->max_attention, m->max_inter}));
     if (!ws) return -1;
     if (verify) {
         uint64_t prop = L * 3 * kMaxVerify * m->max_width;
@@ -1420,7 +1433,7 @@ int plamo_metal_linear(struct plamo_metal *m, const struct plamo_matmul *mm) {
         p.src = as<float>(in);
         ok = launch_gemv(m->stream, w, N, K, p, as<float>(out), 0, 2 * m->cus) == hipSuccess;
     } else if (ok) {
-        const GemmWorkspace *ws = gemm_workspace(m);
+        const GemmWorkspace *ws = gemm_workspace(m, T, K);
         ok = ws && launch_gemm(m->stream, as<float>(in), K, w, N, K, T, as<float>(out), N, ws) ==
                        hipSuccess;
     }
@@ -1447,7 +1460,7 @@ int plamo_metal_mlp(struct plamo_metal *m, const struct mlp *mlp, float *states,
     }
     Buffer &st = m->mlp_state, &nrm = m->mlp_norm, &g = m->mlp_gu, &a = m->mlp_act,
            &b = m->mlp_branch, &norms = m->mlp_norms;
-    const GemmWorkspace *ws = gemm_workspace(m);
+    const GemmWorkspace *ws = gemm_workspace(m, T, std::max(h, I));
     bool ok = ws && ensure(m, st, T * h * 4) && ensure(m, nrm, T * h * 4) &&
               ensure(m, g, T * 2 * I * 4) && ensure(m, a, T * I * 4) && ensure(m, b, T * h * 4) &&
               ensure(m, norms, 2 * h * 2);

@@ -41,26 +41,32 @@ hipError_t launch_embed(hipStream_t, const uint16_t *embedding, const uint32_t *
 // r + swiglu_half are gate/up and y[r] = silu(gate) * up for r < swiglu_half.
 hipError_t launch_gemv(hipStream_t, const uint16_t *w, uint64_t rows, uint64_t cols,
                        const Prologue &pro, float *y, uint64_t swiglu_half, int blocks_hint);
-// Scratch of the split-K GEMM: partial tiles and per-tile arrival counters
-// (zero-initialized; every launch leaves them zero).
+// Scratch of the split-BF16 GEMM: the three BF16 planes of X, split-K partial
+// tiles and per-tile arrival counters (zero-initialized; every launch leaves
+// them zero).
 struct GemmWorkspace {
     float *partial;
     uint64_t partial_floats;
     uint32_t *counter_base;
     uint32_t counters;
+    uint16_t *planes;
+    uint64_t plane_elems;
 };
 struct GemmSplit {
     const float *x;
     uint64_t ldx;
     const uint16_t *w;
-    uint32_t n, k, t, splits;
+    uint32_t n, k, t, tp, splits;
     float *y;
     uint64_t ldy;
     float *partial;
     uint32_t *counters;
+    uint16_t *planes;
 };
 constexpr uint64_t kGemmPartialFloats = 16ull << 20;  // 64 MiB
 constexpr uint32_t kGemmCounters = 8192;
+// BF16 elements of the planes a GEMM of `tokens` rows and `cols` columns needs.
+uint64_t gemm_plane_elems(uint64_t tokens, uint64_t cols);
 // C[t, r] = sum_k X[t, k] * W[r, k]. With a workspace, more than one token
 // and K a multiple of 64: BF16 matrix cores on the exact three-term split of
 // X; otherwise FP32 MFMA with BF16 weights widened in LDS.

@@ -698,85 +698,116 @@ static hipError_t gemm_variant(hipStream_t stream, const float *x, uint64_t x_st
 // three products accumulate in FP32 (v_mfma_f32_32x32x16_bf16). Weights are
 // used as stored, with no widening.
 //
-// Block: 4 waves as 2 x 2, each wave WM x WN tiles of 32 x 32, so the block
-// covers BM = 64 WM token rows by BN = 64 WN weight rows. K advances 64 per
-// stage: the block loads the next stage (X as FP32, W as BF16) into registers
-// while the matrix cores run on the current one, then splits X into its three
-// planes and stores both into the other LDS buffer (one barrier per stage).
-// Grid: (N tiles, M tiles, K splits); with several K splits each block writes
-// its partial tile and the last block of a tile sums them in split order.
+// split_planes_kernel writes the three terms as BF16 planes once per GEMM,
+// stage-major: [K / 32][3][Tp][32] (Tp = T rounded up to the block's row tile,
+// padding rows zero), so one stage of a row tile is contiguous.
+// The GEMM block is 4 waves as 2 x 2, each wave WM x WN tiles of 32 x 32, so
+// a block covers BM = 64 WM token rows by BN = 64 WN weight rows; K advances
+// 32 per stage through double-buffered LDS (two blocks per CU for WN = 2), with
+// three stages in flight in registers. Each block starts its K loop at its
+// own stage (rotating): weight rows are a multiple of 4 KB apart, so blocks in
+// lockstep would all read one memory channel. LDS rows are 64 bytes with their four
+// 16-byte granules XOR-swizzled by row, which keeps the fragment reads and the
+// staging writes free of bank conflicts. Grid: (N tiles, M tiles, K splits);
+// with several K splits each block writes its partial tile and the last block
+// of a tile sums the partials in split order (deterministic).
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-constexpr int kSplitBK = 64;
-constexpr int kSplitPitch = kSplitBK + 8;  // BF16 per LDS row: +16 bytes keeps ds_read_b128 conflict-free
+constexpr int kSplitBK = 32;  // K per stage: four 16-byte granules of BF16 per row
 
 __device__ __forceinline__ uint32_t pack_hi16(uint32_t a, uint32_t b) {
     return (b & 0xffff0000u) | (a >> 16);
 }
+// Physical granule of logical granule q in LDS row r.
+__device__ __forceinline__ uint32_t swizzle(uint32_t r, uint32_t q) {
+    return q ^ ((r ^ (r >> 2)) & 3);
+}
+
+__global__ __launch_bounds__(256) void split_planes_kernel(const float *x, uint64_t ldx,
+                                                           uint32_t rows, uint32_t padded,
+                                                           uint32_t k, uint16_t *planes) {
+    const uint64_t e = ((uint64_t)blockIdx.x * 256 + threadIdx.x) * 8;
+    const uint64_t total = (uint64_t)padded * k;
+    if (e >= total) return;
+    const uint32_t row = (uint32_t)(e / k), col = (uint32_t)(e % k);
+    // Stage-major destination: [col / 32][plane][row][col % 32].
+    const uint64_t at = ((uint64_t)(col / kSplitBK) * 3 * padded + row) * kSplitBK + col % kSplitBK;
+    const uint64_t pl = (uint64_t)padded * kSplitBK;
+    f32x4 a = {0.0f, 0.0f, 0.0f, 0.0f}, b = a;
+    if (row < rows) {
+        a = *(const f32x4 *)(x + row * ldx + col);
+        b = *(const f32x4 *)(x + row * ldx + col + 4);
+    }
+    const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+    uint32_t h[8], md[8], lo[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        h[i] = __float_as_uint(v[i]) & 0xffff0000u;
+        const float r = v[i] - __uint_as_float(h[i]);
+        md[i] = __float_as_uint(r) & 0xffff0000u;
+        lo[i] = __float_as_uint(r - __uint_as_float(md[i]));
+    }
+    *(u32x4 *)(planes + at) = u32x4{pack_hi16(h[0], h[1]), pack_hi16(h[2], h[3]),
+                                    pack_hi16(h[4], h[5]), pack_hi16(h[6], h[7])};
+    *(u32x4 *)(planes + at + pl) = u32x4{pack_hi16(md[0], md[1]), pack_hi16(md[2], md[3]),
+                                         pack_hi16(md[4], md[5]), pack_hi16(md[6], md[7])};
+    *(u32x4 *)(planes + at + 2 * pl) = u32x4{pack_hi16(lo[0], lo[1]), pack_hi16(lo[2], lo[3]),
+                                             pack_hi16(lo[4], lo[5]), pack_hi16(lo[6], lo[7])};
+}
 
 template <int WM, int WN>
-__global__ __launch_bounds__(256) void gemm_split_kernel(GemmSplit g) {
+__global__ __launch_bounds__(256, WN > 2 ? 1 : 2) void gemm_split_kernel(GemmSplit g) {
     constexpr int BM = 64 * WM, BN = 64 * WN;
-    constexpr int FX = BM / 4;        // X floats staged per thread per stage
-    constexpr int TX = kSplitBK / FX; // threads per X row
-    constexpr int FW = BN / 4;        // W BF16 staged per thread per stage
-    constexpr int TW = kSplitBK / FW; // threads per W row
-    constexpr int BUF = (3 * BM + BN) * kSplitPitch;  // BF16 per LDS buffer
-    extern __shared__ uint16_t lds[];
+    constexpr int AG = 3 * BM * 4, WG = BN * 4, SG = AG + WG;  // granules per stage
+    constexpr int APT = AG / 256, WPT = WG / 256;               // granules per thread
+    extern __shared__ u32x4 lds[];                               // [2][SG]
     __shared__ int is_last;
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const uint32_t wm = wave >> 1, wn = wave & 1;
     const uint32_t m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
     const uint32_t kper = g.k / g.splits;
-    const uint32_t kbeg = blockIdx.z * kper, kend = kbeg + kper;
+    const uint32_t kbeg = blockIdx.z * kper, nst = kper / kSplitBK;
+    const uint32_t first = blockIdx.x % nst;  // rotation of this block's stages
+    const uint64_t stage_elems = 3ull * g.tp * kSplitBK;  // planes of one stage
 
-    // Staging assignment (clamped rows: rows past T or N load a valid row whose
-    // results are never stored).
-    const uint32_t xr = threadIdx.x / TX, xc = (threadIdx.x % TX) * FX;
-    const uint32_t wr = threadIdx.x / TW, wc = (threadIdx.x % TW) * FW;
-    const float *xsrc = g.x + (uint64_t)min(m0 + xr, g.t - 1) * g.ldx + xc;
-    const uint16_t *wsrc = g.w + (uint64_t)min(n0 + wr, g.n - 1) * g.k + wc;
-    const bool xvalid = m0 + xr < g.t;
-    f32x4 xv[FX / 4];
-    u32x4 wv[FW / 8];
-    auto load = [&](uint32_t k) {
+    // Staging: granule G = threadIdx + 256 i of the stage; A granules first.
+    const uint16_t *asrc[APT];
+    uint32_t adst[APT];
 #pragma unroll
-        for (int i = 0; i < FX / 4; ++i) xv[i] = *(const f32x4 *)(xsrc + k + 4 * i);
+    for (int i = 0; i < APT; ++i) {
+        const uint32_t G = threadIdx.x + 256 * i, R = G / 4, q = G % 4;
+        const uint32_t p = R / BM, r = R % BM;
+        asrc[i] = g.planes + ((uint64_t)p * g.tp + m0 + r) * kSplitBK + 8 * q;
+        adst[i] = R * 4 + swizzle(R, q);
+    }
+    const uint16_t *wsrc[WPT];
+    uint32_t wdst[WPT];
 #pragma unroll
-        for (int i = 0; i < FW / 8; ++i)
-            wv[i] = __builtin_nontemporal_load((const u32x4 *)(wsrc + k) + i);
+    for (int i = 0; i < WPT; ++i) {
+        const uint32_t G = threadIdx.x + 256 * i, r = G / 4, q = G % 4;
+        wsrc[i] = g.w + (uint64_t)min(n0 + r, g.n - 1) * g.k + 8 * q;
+        wdst[i] = AG + r * 4 + swizzle(r, q);
+    }
+    u32x4 av[3][APT], wv[3][WPT];
+    auto load = [&](int slot, uint32_t stage) {
+        uint32_t s = first + min(stage, nst - 1);
+        s = s < nst ? s : s - nst;
+        const uint32_t ks = kbeg / kSplitBK + s;
+#pragma unroll
+        for (int i = 0; i < APT; ++i)
+            av[slot][i] = *(const u32x4 *)(asrc[i] + (uint64_t)ks * stage_elems);
+#pragma unroll
+        for (int i = 0; i < WPT; ++i)
+            wv[slot][i] =
+                __builtin_nontemporal_load((const u32x4 *)(wsrc[i] + (uint64_t)ks * kSplitBK));
     };
-    auto store = [&](int buf) {
-        uint16_t *xl = lds + buf * BUF;
-        uint16_t *wl = xl + 3 * BM * kSplitPitch;
+    auto store = [&](int slot, int buf) {
+        u32x4 *st = lds + buf * SG;
 #pragma unroll
-        for (int i = 0; i < FX / 8; ++i) {
-            uint32_t h[8], md[8], lo[8];
+        for (int i = 0; i < APT; ++i) st[adst[i]] = av[slot][i];
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const f32x4 q = xv[2 * i + e / 4];
-                float x = e % 4 == 0 ? q.x : e % 4 == 1 ? q.y : e % 4 == 2 ? q.z : q.w;
-                x = xvalid ? x : 0.0f;
-                const uint32_t u = __float_as_uint(x);
-                h[e] = u & 0xffff0000u;
-                const float r = x - __uint_as_float(h[e]);
-                md[e] = __float_as_uint(r) & 0xffff0000u;
-                lo[e] = __float_as_uint(r - __uint_as_float(md[e]));
-            }
-            const uint32_t col = xc + 8 * i;
-            u32x4 ph = {pack_hi16(h[0], h[1]), pack_hi16(h[2], h[3]), pack_hi16(h[4], h[5]),
-                        pack_hi16(h[6], h[7])};
-            u32x4 pm = {pack_hi16(md[0], md[1]), pack_hi16(md[2], md[3]),
-                        pack_hi16(md[4], md[5]), pack_hi16(md[6], md[7])};
-            u32x4 pl = {pack_hi16(lo[0], lo[1]), pack_hi16(lo[2], lo[3]),
-                        pack_hi16(lo[4], lo[5]), pack_hi16(lo[6], lo[7])};
-            *(u32x4 *)(xl + (0 * BM + xr) * kSplitPitch + col) = ph;
-            *(u32x4 *)(xl + (1 * BM + xr) * kSplitPitch + col) = pm;
-            *(u32x4 *)(xl + (2 * BM + xr) * kSplitPitch + col) = pl;
-        }
-#pragma unroll
-        for (int i = 0; i < FW / 8; ++i) *(u32x4 *)(wl + wr * kSplitPitch + wc + 8 * i) = wv[i];
+        for (int i = 0; i < WPT; ++i) st[wdst[i]] = wv[slot][i];
     };
 
     f32x16 acc[WM][WN];
@@ -787,31 +818,24 @@ __global__ __launch_bounds__(256) void gemm_split_kernel(GemmSplit g) {
 #pragma unroll
             for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
 
-    load(kbeg);
-    store(0);
-    __syncthreads();
-    int buf = 0;
-    for (uint32_t k = kbeg; k < kend; k += kSplitBK) {
-        // Next stage (clamped to the last one: unconditional, so the compiler
-        // keeps exact wait counts).
-        load(min(k + kSplitBK, kend - kSplitBK));
-        const uint16_t *xl = lds + buf * BUF;
-        const uint16_t *wl = xl + 3 * BM * kSplitPitch;
+    auto compute = [&](int buf) {
+        const u32x4 *st = lds + buf * SG;
 #pragma unroll
         for (int ks = 0; ks < kSplitBK / 16; ++ks) {
-            const uint32_t kk = ks * 16 + 8 * (lane >> 5);
+            const uint32_t q = 2 * ks + (lane >> 5);
             bf16x8 a[3][WM], b[WN];
 #pragma unroll
             for (int i = 0; i < WM; ++i) {
-                const uint32_t row = wm * 32 * WM + 32 * i + (lane & 31);
 #pragma unroll
-                for (int p = 0; p < 3; ++p)
-                    a[p][i] = *(const bf16x8 *)(xl + (p * BM + row) * kSplitPitch + kk);
+                for (int p = 0; p < 3; ++p) {
+                    const uint32_t R = p * BM + wm * 32 * WM + 32 * i + (lane & 31);
+                    a[p][i] = __builtin_bit_cast(bf16x8, st[R * 4 + swizzle(R, q)]);
+                }
             }
 #pragma unroll
             for (int j = 0; j < WN; ++j) {
-                const uint32_t row = wn * 32 * WN + 32 * j + (lane & 31);
-                b[j] = *(const bf16x8 *)(wl + row * kSplitPitch + kk);
+                const uint32_t r = wn * 32 * WN + 32 * j + (lane & 31);
+                b[j] = __builtin_bit_cast(bf16x8, st[AG + r * 4 + swizzle(r, q)]);
             }
 #pragma unroll
             for (int p = 0; p < 3; ++p)
@@ -822,57 +846,80 @@ __global__ __launch_bounds__(256) void gemm_split_kernel(GemmSplit g) {
                         acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[p][i], b[j],
                                                                              acc[i][j], 0, 0, 0);
         }
-        if (k + kSplitBK < kend) store(buf ^ 1);
+    };
+
+    // Stage j lives in register slot j % 3 and LDS buffer j % 2. Loads are
+    // unconditional (clamped to the last stage) so the compiler keeps exact
+    // wait counts; the step count is padded to a multiple of three.
+    load(0, 0);
+    load(1, 1);
+    load(2, 2);
+    store(0, 0);
+    __syncthreads();
+    int buf = 0;
+    auto step = [&](uint32_t j, int slot) {
+        load(slot, j + 3);
+        if (j < nst) {
+            compute(buf);
+            if (j + 1 < nst) store((slot + 1) % 3, buf ^ 1);
+        }
         __syncthreads();
         buf ^= 1;
+    };
+    for (uint32_t j = 0; j < nst; j += 3) {
+        step(j, 0);
+        step(j + 1, 1);
+        step(j + 2, 2);
     }
 
     // D layout of v_mfma_f32_32x32x16: value v of lane l is row
     // 8 (v / 4) + 4 (l / 32) + v % 4, column l % 32 of the 32 x 32 tile.
     const uint32_t tile = blockIdx.y * gridDim.x + blockIdx.x;
     const uint32_t tiles = gridDim.x * gridDim.y;
-    if (g.splits == 1) {
+    if (g.splits > 1) {
+        // Partial tile, laid out [split][tile][wave][i][j][v][lane] (coalesced).
+        float *part = g.partial + ((uint64_t)blockIdx.z * tiles + tile) * (BM * BN);
 #pragma unroll
         for (int i = 0; i < WM; ++i)
 #pragma unroll
-            for (int j = 0; j < WN; ++j) {
-                const uint32_t col = n0 + wn * 32 * WN + 32 * j + (lane & 31);
+            for (int j = 0; j < WN; ++j)
 #pragma unroll
-                for (int v = 0; v < 16; ++v) {
-                    const uint32_t row =
-                        m0 + wm * 32 * WM + 32 * i + 8 * (v / 4) + 4 * (lane >> 5) + v % 4;
-                    if (row < g.t && col < g.n) g.y[(uint64_t)row * g.ldy + col] = acc[i][j][v];
-                }
-            }
-        return;
+                for (int v = 0; v < 16; ++v)
+                    part[(((wave * WM + i) * WN + j) * 16 + v) * 64 + lane] = acc[i][j][v];
+        __threadfence();
+        __syncthreads();
+        if (threadIdx.x == 0) is_last = atomicAdd(&g.counters[tile], 1u) + 1 == g.splits;
+        __syncthreads();
+        if (!is_last) return;
+        __threadfence();
+        // Sum the partials in split order; each split's 64 values are loaded
+        // together.
+        const float *base = g.partial + (uint64_t)tile * (BM * BN) + wave * WM * WN * 1024 + lane;
+        float sum[WM][WN][16];
+#pragma unroll
+        for (int i = 0; i < WM; ++i)
+#pragma unroll
+            for (int j = 0; j < WN; ++j)
+#pragma unroll
+                for (int v = 0; v < 16; ++v) sum[i][j][v] = base[((i * WN + j) * 16 + v) * 64];
+        for (uint32_t sp = 1; sp < g.splits; ++sp) {
+            const float *ps = base + (uint64_t)sp * tiles * (BM * BN);
+#pragma unroll
+            for (int i = 0; i < WM; ++i)
+#pragma unroll
+                for (int j = 0; j < WN; ++j)
+#pragma unroll
+                    for (int v = 0; v < 16; ++v)
+                        sum[i][j][v] = sum[i][j][v] + ps[((i * WN + j) * 16 + v) * 64];
+        }
+#pragma unroll
+        for (int i = 0; i < WM; ++i)
+#pragma unroll
+            for (int j = 0; j < WN; ++j)
+#pragma unroll
+                for (int v = 0; v < 16; ++v) acc[i][j][v] = sum[i][j][v];
+        if (threadIdx.x == 0) g.counters[tile] = 0;
     }
-    // Partial tile, laid out [split][tile][wave][i][j][v][lane] (coalesced).
-    float *part = g.partial + ((uint64_t)blockIdx.z * tiles + tile) * (BM * BN);
-#pragma unroll
-    for (int i = 0; i < WM; ++i)
-#pragma unroll
-        for (int j = 0; j < WN; ++j)
-#pragma unroll
-            for (int v = 0; v < 16; ++v)
-                part[(((wave * WM + i) * WN + j) * 16 + v) * 64 + lane] = acc[i][j][v];
-    __threadfence();
-    __syncthreads();
-    if (threadIdx.x == 0) is_last = atomicAdd(&g.counters[tile], 1u) + 1 == g.splits;
-    __syncthreads();
-    if (!is_last) return;
-    __threadfence();
-#pragma unroll
-    for (int i = 0; i < WM; ++i)
-#pragma unroll
-        for (int j = 0; j < WN; ++j)
-#pragma unroll
-            for (int v = 0; v < 16; ++v) {
-                const uint64_t at = (((wave * WM + i) * WN + j) * 16 + v) * 64 + lane;
-                float sum = g.partial[(uint64_t)tile * (BM * BN) + at];
-                for (uint32_t sp = 1; sp < g.splits; ++sp)
-                    sum = sum + g.partial[((uint64_t)sp * tiles + tile) * (BM * BN) + at];
-                acc[i][j][v] = sum;
-            }
 #pragma unroll
     for (int i = 0; i < WM; ++i)
 #pragma unroll
@@ -885,18 +932,19 @@ __global__ __launch_bounds__(256) void gemm_split_kernel(GemmSplit g) {
                 if (row < g.t && col < g.n) g.y[(uint64_t)row * g.ldy + col] = acc[i][j][v];
             }
         }
-    if (threadIdx.x == 0) g.counters[tile] = 0;
 }
 
 template <int WM, int WN>
 static hipError_t gemm_split_variant(hipStream_t stream, GemmSplit g, const GemmWorkspace &ws) {
     constexpr uint32_t BM = 64 * WM, BN = 64 * WN;
     const uint32_t nt = (g.n + BN - 1) / BN, mt = (g.t + BM - 1) / BM;
-    const uint32_t tiles = nt * mt, kblocks = g.k / kSplitBK;
-    // Enough blocks for the 256 CUs, each split at least two stages long.
+    const uint32_t tiles = nt * mt, stages = g.k / kSplitBK;
+    g.tp = mt * BM;
+    if ((uint64_t)3 * g.tp * g.k > ws.plane_elems) return hipErrorInvalidValue;
+    // Two blocks per CU: aim for 512 blocks, each split at least four stages.
     uint32_t splits = 1;
-    while (tiles * splits < 256 && kblocks % (2 * splits) == 0 && kblocks / (2 * splits) >= 2 &&
-           splits < 16)
+    while (tiles * splits < 512 && stages % (2 * splits) == 0 && stages / (2 * splits) >= 4 &&
+           splits < 8)
         splits *= 2;
     if (splits > 1 && ((uint64_t)splits * tiles * BM * BN > ws.partial_floats ||
                        tiles > ws.counters))
@@ -904,7 +952,11 @@ static hipError_t gemm_split_variant(hipStream_t stream, GemmSplit g, const Gemm
     g.splits = splits;
     g.partial = ws.partial;
     g.counters = ws.counter_base;
-    const size_t lds = 2 * (size_t)(3 * BM + BN) * kSplitPitch * sizeof(uint16_t);
+    g.planes = ws.planes;
+    const uint64_t elems = (uint64_t)g.tp * g.k;
+    split_planes_kernel<<<(unsigned)((elems / 8 + 255) / 256), 256, 0, stream>>>(
+        g.x, g.ldx, g.t, g.tp, g.k, ws.planes);
+    const size_t lds = 2 * (size_t)(3 * BM * 4 + BN * 4) * sizeof(u32x4);
     static bool attr = false;
     if (!attr) {
         hipError_t e = hipFuncSetAttribute((const void *)gemm_split_kernel<WM, WN>,
@@ -916,17 +968,23 @@ static hipError_t gemm_split_variant(hipStream_t stream, GemmSplit g, const Gemm
     return hipGetLastError();
 }
 
-bool gemm_split_supported(const float *x, uint64_t x_stride, const uint16_t *w, uint64_t cols) {
-    return cols % kSplitBK == 0 && x_stride % 4 == 0 && !((uintptr_t)x & 15) &&
+static bool gemm_split_supported(const float *x, uint64_t x_stride, const uint16_t *w,
+                                 uint64_t cols) {
+    return cols % (2 * kSplitBK) == 0 && x_stride % 4 == 0 && !((uintptr_t)x & 15) &&
            !((uintptr_t)w & 15) && cols <= (1u << 30);
+}
+
+uint64_t gemm_plane_elems(uint64_t tokens, uint64_t cols) {
+    return 3 * ((tokens + 127) / 128 * 128) * cols;
 }
 
 hipError_t launch_gemm(hipStream_t stream, const float *x, uint64_t x_stride, const uint16_t *w,
                        uint64_t rows, uint64_t cols, uint64_t tokens, float *y,
                        uint64_t y_stride, const GemmWorkspace *ws) {
     if (!tokens || !rows) return hipSuccess;
-    if (ws && tokens > 1 && rows < (1u << 31) && tokens < (1u << 31) &&
-        gemm_split_supported(x, x_stride, w, cols)) {
+    if (ws && ws->planes && tokens > 1 && rows < (1u << 31) && tokens < (1u << 31) &&
+        gemm_split_supported(x, x_stride, w, cols) &&
+        gemm_plane_elems(tokens, cols) <= ws->plane_elems) {
         GemmSplit g{};
         g.x = x;
         g.ldx = x_stride;
@@ -936,8 +994,14 @@ hipError_t launch_gemm(hipStream_t stream, const float *x, uint64_t x_stride, co
         g.t = (uint32_t)tokens;
         g.y = y;
         g.ldy = y_stride;
-        if (tokens <= 64) return gemm_split_variant<1, 2>(stream, g, *ws);
-        return gemm_split_variant<2, 2>(stream, g, *ws);
+        // Wide tiles (64 x 128 per wave) when there are enough of them: fewer
+        // LDS bytes per MFMA and half the re-reads of X.
+        const bool wide = (rows + 255) / 256 * ((tokens + 127) / 128) >= 64;
+        if (tokens <= 64)
+            return wide ? gemm_split_variant<1, 4>(stream, g, *ws)
+                        : gemm_split_variant<1, 2>(stream, g, *ws);
+        return wide ? gemm_split_variant<2, 4>(stream, g, *ws)
+                    : gemm_split_variant<2, 2>(stream, g, *ws);
     }
     if (tokens <= 16) return gemm_variant<16, 64>(stream, x, x_stride, w, rows, cols, tokens, y, y_stride);
     return gemm_variant<64, 64>(stream, x, x_stride, w, rows, cols, tokens, y, y_stride);
