@@ -35,7 +35,6 @@ namespace {
 constexpr float kAttentionOffset = 0.2f;                  // src/layer.s:51
 constexpr float kMlpOffset = 0.08944271909999159f;        // src/model.s:111
 constexpr uint64_t kInitialRows = 8192;
-constexpr uint32_t kDecodeSplits = 8;
 constexpr uint64_t kMaxPrompt = 4096;                     // runtime/metal_model.m:540
 
 struct Range {
@@ -96,6 +95,7 @@ struct plamo_metal {
     uint16_t *final_norm = nullptr;
     uint64_t max_width = 0, max_qkv = 0, max_attention = 0, max_inter = 0, max_cols = 0;
     uint64_t max_partial = 0;  // qh * (dim + 2) over layers
+    uint32_t max_splits = 1;   // attention blocks per KV head at full capacity
 
     StepParams *params_host = nullptr, *params_dev = nullptr;
     // Decode workspace.
@@ -335,6 +335,7 @@ int prepare(plamo_metal *m, struct model *model) {
     uint64_t h = model->hidden;
     m->layers.resize(model->count);
     m->max_width = m->max_qkv = m->max_attention = m->max_inter = m->max_partial = 0;
+    m->max_splits = 1;
     m->max_cols = h;
     for (uint64_t i = 0; i < model->count; ++i) {
         const struct layer *l = model->layers[i];
@@ -422,6 +423,7 @@ int prepare(plamo_metal *m, struct model *model) {
         m->max_attention = std::max<uint64_t>(m->max_attention, (uint64_t)d.qh * d.dim);
         m->max_inter = std::max<uint64_t>(m->max_inter, d.inter);
         m->max_partial = std::max<uint64_t>(m->max_partial, (uint64_t)d.qh * (d.dim + 2));
+        m->max_splits = std::max(m->max_splits, decode_attention_splits(d.capacity));
         m->max_cols = std::max<uint64_t>(m->max_cols, std::max<uint64_t>(d.inter, (uint64_t)d.qh * d.dim));
     }
     // The embedding is read one row per token on the device: keep the table
@@ -468,7 +470,7 @@ int prepare(plamo_metal *m, struct model *model) {
     m->branch = dev_alloc<float>(m, h);
     m->act = dev_alloc<float>(m, m->max_inter);
     m->down_out = dev_alloc<float>(m, h);
-    m->partial = dev_alloc<float>(m, m->max_partial * kDecodeSplits);
+    m->partial = dev_alloc<float>(m, m->max_partial * m->max_splits);
     m->counters = dev_alloc<uint32_t>(m, 256);
     m->outbox_floats = V + 2 * h + L * 3 * m->max_width;
     m->outbox = dev_alloc<float>(m, m->outbox_floats);
@@ -629,7 +631,7 @@ int encode_decode(plamo_metal *m, struct model *model, const DecodePlan &plan, i
             da.qh = d.qh;
             da.kh = d.kh;
             da.dim = d.dim;
-            da.splits = kDecodeSplits;
+            da.splits = decode_attention_splits(d.rows);
             HIP_TRY(m, launch_decode_attention(s, da));
             ++n;
         } else {
@@ -1548,7 +1550,7 @@ extern "C" int plamo_hip_time_kernel(struct plamo_metal *m, struct model *model,
             da.qh = d.qh;
             da.kh = d.kh;
             da.dim = d.dim;
-            da.splits = kDecodeSplits;
+            da.splits = decode_attention_splits(d.rows);
             return launch_decode_attention(s, da);
         }
         }

@@ -121,6 +121,9 @@ struct DecodeAttention {
 };
 hipError_t launch_decode_attention(hipStream_t, const DecodeAttention &);
 bool decode_attention_supported(uint32_t dim, uint32_t group);
+// Blocks per KV head that cover `rows` cache rows (DecodeAttention::splits
+// must be at least this for the largest row count of the launch).
+uint32_t decode_attention_splits(uint64_t rows);
 
 // General causal attention for `tokens` query rows. Key j of query t is the
 // virtual row j of [cache rows 0..prefix) ++ [new rows 0..tokens). With

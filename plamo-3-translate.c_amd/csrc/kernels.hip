@@ -81,6 +81,37 @@ __device__ __forceinline__ float rows_max(float v) {
 __device__ __forceinline__ float wave_sum(float v) { return rows_sum(row_sum16(v)); }
 __device__ __forceinline__ float wave_max(float v) { return rows_max(row_max16(v)); }
 
+// Cross-block hand-off without a device-scope fence (which writes back and
+// invalidates the whole L2): partials are written through to the coherence
+// point (agent-scope atomic stores), the writer waits for its stores to
+// complete before it counts itself in, and the last block reads the partials
+// from the coherence point (agent-scope atomic loads), past any stale L2 copy.
+__device__ __forceinline__ void store_through(float *p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float load_through(const float *p) {
+    return __hip_atomic_load(const_cast<float *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void wait_stores() {
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+// Returns true in the block that completes a group of `expected` blocks
+// (counter left at zero for the next launch); call from all threads.
+__device__ __forceinline__ bool arrive_last(uint32_t *counter, uint32_t expected, int *flag) {
+    wait_stores();
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const uint32_t done =
+            __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        *flag = done + 1 == expected;
+        if (*flag) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    return *flag;
+}
+
 // 1 / sqrt(mean(x^2) + 1e-6) for a 256-thread block (tests/rmsnorm_reference.s:8-21
 // arithmetic per element; the sum is a fixed tree).
 __device__ float block_rms_inverse(const float *x, uint32_t n, float *red) {
@@ -192,16 +223,13 @@ hipError_t launch_embed(hipStream_t stream, const uint16_t *embedding, const uin
 // rows with 16-byte non-temporal loads, FMA-accumulates against the LDS copy,
 // and butterfly-reduces. With SWIGLU the pair is (gate row r, up row r+half)
 // and the output is silu(gate) * up (tests/activation_reference.s:99-126).
-// Loads one batch of a wave's stream: 4 chunks (of 8 BF16 each) per lane of
-// the row pair at iteration `it` (pairs advance every `nb` iterations).
+// Loads one batch of a wave's stream: 4 chunks (of 8 BF16 each) per lane from
+// chunk c of the row pair.
 template <bool SWIGLU>
-__device__ __forceinline__ bool gemv_batch(const uint16_t *w, uint64_t rows, uint64_t cols,
-                                           uint64_t half, uint64_t pairs, uint64_t p0,
-                                           uint64_t step, uint64_t nb, uint64_t it, uint32_t lane,
-                                           u32x4 (&qa)[4], u32x4 (&qb)[4]) {
-    const uint64_t pair = p0 + (it / nb) * step;
-    if (pair >= pairs) return false;
-    const uint64_t chunks = cols / 8, c = lane + (it % nb) * 256;
+__device__ __forceinline__ void gemv_load(const uint16_t *w, uint64_t rows, uint64_t cols,
+                                          uint64_t half, uint64_t pairs, uint64_t pair,
+                                          uint64_t c, u32x4 (&qa)[4], u32x4 (&qb)[4]) {
+    const uint64_t chunks = cols / 8;
     const uint64_t ra = SWIGLU ? pair : 2 * pair;
     const uint64_t rb0 = SWIGLU ? pair + half : 2 * pair + 1;
     const uint64_t rb = rb0 < rows ? rb0 : ra;
@@ -212,7 +240,6 @@ __device__ __forceinline__ bool gemv_batch(const uint16_t *w, uint64_t rows, uin
             qa[j] = __builtin_nontemporal_load(va + c + 64 * j);
             qb[j] = __builtin_nontemporal_load(vb + c + 64 * j);
         }
-    return true;
 }
 
 __device__ __forceinline__ void gemv_accumulate(const float *xs, uint64_t chunks, uint64_t c,
@@ -255,9 +282,9 @@ __device__ __forceinline__ void gemv_store(float *y, uint64_t rows, uint64_t pai
 
 // Decode projections with a norm prologue (or a raw input the register GEMV
 // does not cover). Vector-memory loads complete in order on CDNA, so the
-// prologue's own loads are issued first, then the first weight batch, so the
-// norm's reductions overlap the weights in flight. The weight stream is
-// software-pipelined: batch i+1 is requested before batch i is consumed.
+// prologue's own loads are issued first, then the first three weight batches,
+// so the norm's reductions overlap the weights in flight. The weight stream
+// keeps three batches in flight: batch i+3 is requested as batch i is consumed.
 // With SWIGLU the pair is (gate row r, up row r+half) and the output is
 // silu(gate) * up (tests/activation_reference.s:99-126).
 template <bool VEC, bool SWIGLU>
@@ -273,6 +300,8 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(const uint16_t *__restri
     const uint64_t chunks = cols / 8, nb = (chunks + 255) / 256;
     const uint64_t step = (uint64_t)gridDim.x * 4;
     const uint64_t p0 = (uint64_t)blockIdx.x * 4 + wave;
+    // Batches of this wave: nb per row pair, pairs p0, p0 + step, ...
+    const uint64_t total = p0 < pairs ? ((pairs - 1 - p0) / step + 1) * nb : 0;
     // One-round-trip prologue: contiguous 16-element slices per thread.
     const bool fast = pro.w && n % 16 == 0 && n <= 16 * kThreads &&
                       !(((uintptr_t)pro.src | (uintptr_t)pro.w |
@@ -315,8 +344,17 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(const uint16_t *__restri
         }
     }
     __builtin_amdgcn_sched_barrier(0);
-    u32x4 qa0[4], qb0[4], qa1[4], qb1[4];
-    if (VEC) gemv_batch<SWIGLU>(w, rows, cols, half, pairs, p0, step, nb, 0, lane, qa0, qb0);
+    // Three batches in flight: the first three go out before the prologue.
+    u32x4 qa0[4], qb0[4], qa1[4], qb1[4], qa2[4], qb2[4];
+    auto issue = [&](uint64_t it, u32x4(&qa)[4], u32x4(&qb)[4]) {
+        gemv_load<SWIGLU>(w, rows, cols, half, pairs, p0 + (it / nb) * step,
+                          lane + (it % nb) * 256, qa, qb);
+    };
+    if (VEC) {
+        if (total > 0) issue(0, qa0, qb0);
+        if (total > 1) issue(1, qa1, qb1);
+        if (total > 2) issue(2, qa2, qb2);
+    }
     __builtin_amdgcn_sched_barrier(0);
 
     if (fast) {
@@ -392,22 +430,36 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(const uint16_t *__restri
 
     if (VEC) {
         float acc_a = 0.0f, acc_b = 0.0f;
-        for (uint64_t it = 0;; it += 2) {
-            const bool more1 = gemv_batch<SWIGLU>(w, rows, cols, half, pairs, p0, step, nb, it + 1, lane, qa1, qb1);
-            if (p0 + (it / nb) * step >= pairs) break;
-            gemv_accumulate(xs, chunks, lane + (it % nb) * 256, qa0, qb0, acc_a, acc_b);
+        auto consume = [&](uint64_t it, const u32x4(&qa)[4], const u32x4(&qb)[4]) {
+            gemv_accumulate(xs, chunks, lane + (it % nb) * 256, qa, qb, acc_a, acc_b);
             if (it % nb == nb - 1) {
                 gemv_store<SWIGLU>(y, rows, p0 + (it / nb) * step, acc_a, acc_b, lane);
                 acc_a = acc_b = 0.0f;
             }
-            if (!more1) break;
-            gemv_batch<SWIGLU>(w, rows, cols, half, pairs, p0, step, nb, it + 2, lane, qa0, qb0);
-            gemv_accumulate(xs, chunks, lane + ((it + 1) % nb) * 256, qa1, qb1, acc_a, acc_b);
-            if ((it + 1) % nb == nb - 1) {
-                gemv_store<SWIGLU>(y, rows, p0 + ((it + 1) / nb) * step, acc_a, acc_b, lane);
-                acc_a = acc_b = 0.0f;
-            }
+        };
+        // Steady state: every refill is a real batch, issued unconditionally
+        // (so the compiler keeps exact wait counts); the tail has no refills
+        // past the stream.
+        uint64_t it = 0;
+        for (; it + 5 < total; it += 3) {
+            consume(it, qa0, qb0);
+            issue(it + 3, qa0, qb0);
+            consume(it + 1, qa1, qb1);
+            issue(it + 4, qa1, qb1);
+            consume(it + 2, qa2, qb2);
+            issue(it + 5, qa2, qb2);
         }
+        if (it < total) {
+            consume(it, qa0, qb0);
+            if (it + 3 < total) issue(it + 3, qa0, qb0);
+        }
+        if (it + 1 < total) {
+            consume(it + 1, qa1, qb1);
+            if (it + 4 < total) issue(it + 4, qa1, qb1);
+        }
+        if (it + 2 < total) consume(it + 2, qa2, qb2);
+        if (it + 3 < total) consume(it + 3, qa0, qb0);
+        if (it + 4 < total) consume(it + 4, qa1, qb1);
     } else {
         for (uint64_t p = p0; p < pairs; p += step) {
             const uint64_t ra = SWIGLU ? p : 2 * p;
@@ -885,13 +937,9 @@ __global__ __launch_bounds__(256, WN > 2 ? 1 : 2) void gemm_split_kernel(GemmSpl
             for (int j = 0; j < WN; ++j)
 #pragma unroll
                 for (int v = 0; v < 16; ++v)
-                    part[(((wave * WM + i) * WN + j) * 16 + v) * 64 + lane] = acc[i][j][v];
-        __threadfence();
-        __syncthreads();
-        if (threadIdx.x == 0) is_last = atomicAdd(&g.counters[tile], 1u) + 1 == g.splits;
-        __syncthreads();
-        if (!is_last) return;
-        __threadfence();
+                    store_through(part + (((wave * WM + i) * WN + j) * 16 + v) * 64 + lane,
+                                  acc[i][j][v]);
+        if (!arrive_last(&g.counters[tile], g.splits, &is_last)) return;
         // Sum the partials in split order; each split's 64 values are loaded
         // together.
         const float *base = g.partial + (uint64_t)tile * (BM * BN) + wave * WM * WN * 1024 + lane;
@@ -901,7 +949,8 @@ __global__ __launch_bounds__(256, WN > 2 ? 1 : 2) void gemm_split_kernel(GemmSpl
 #pragma unroll
             for (int j = 0; j < WN; ++j)
 #pragma unroll
-                for (int v = 0; v < 16; ++v) sum[i][j][v] = base[((i * WN + j) * 16 + v) * 64];
+                for (int v = 0; v < 16; ++v)
+                    sum[i][j][v] = load_through(base + ((i * WN + j) * 16 + v) * 64);
         for (uint32_t sp = 1; sp < g.splits; ++sp) {
             const float *ps = base + (uint64_t)sp * tiles * (BM * BN);
 #pragma unroll
@@ -910,7 +959,7 @@ __global__ __launch_bounds__(256, WN > 2 ? 1 : 2) void gemm_split_kernel(GemmSpl
                 for (int j = 0; j < WN; ++j)
 #pragma unroll
                     for (int v = 0; v < 16; ++v)
-                        sum[i][j][v] = sum[i][j][v] + ps[((i * WN + j) * 16 + v) * 64];
+                        sum[i][j][v] = sum[i][j][v] + load_through(ps + ((i * WN + j) * 16 + v) * 64);
         }
 #pragma unroll
         for (int i = 0; i < WM; ++i)
@@ -918,7 +967,6 @@ __global__ __launch_bounds__(256, WN > 2 ? 1 : 2) void gemm_split_kernel(GemmSpl
             for (int j = 0; j < WN; ++j)
 #pragma unroll
                 for (int v = 0; v < 16; ++v) acc[i][j][v] = sum[i][j][v];
-        if (threadIdx.x == 0) g.counters[tile] = 0;
     }
 #pragma unroll
     for (int i = 0; i < WM; ++i)
@@ -1145,67 +1193,66 @@ hipError_t launch_qkv_post(hipStream_t stream, const QkvPost &a) {
 }
 
 // ---------------------------------------------------------------- decode attention
-// Flash-decoding: the group's query heads share one pass over the KV head's
-// rows; scores are FMA chains (tests/attention_reference.s:27-40) and the
-// softmax is online, with the reference exponential.
-// One block of 8 waves per KV head. A wave takes RW rows per pass: for the
-// scores, 16 lanes share a row (DIM/16 dims each, the 16 partial dots are
-// reduced within the 16-lane group) and each lane covers RW/4 rows; for the
-// values, each lane owns DIM/64 adjacent columns. Vector-memory loads return
-// in order, so the loads are issued in the order they are consumed: first
-// what does not depend on the step's row count (query/key heads and norm
-// weights), then the RoPE row, then two passes of K/V rows; pass p+2 is
-// requested before pass p+1 is consumed. Contexts longer than kRowsPerBlock
-// rows are split across up to `splits` blocks per KV head and merged by the
-// last one.
+// Decode attention for one KV head group per block, with the reference's
+// softmax (tests/attention_reference.s:8-112: scores as FMA chains times
+// 1/sqrt(d), the maximum over all rows, exp, sum, weighted value sum).
+// Blocks of 8 waves take up to kRowsPerBlock rows; longer contexts are split
+// across blocks whose partials (max, sum, weighted values) the last block of
+// the KV head merges.
+//
+// Phase 0: the count-independent loads go out first (vector-memory loads
+// return in order): the query heads, the new key/value and their norm
+// weights; then the RoPE row of the step's position; then two passes of K and
+// V rows. The query heads are normalized and rotated into LDS while the rows
+// are in flight; the last wave normalizes, rotates and appends the new row.
+// Phase 1: scores. For each pass a wave takes RW rows, 16 lanes per row (each
+// lane DIM/16 dims), reduced with DPP; scores go to LDS [row][head].
+// Phase 2: per head (one wave each) the maximum, exp in place, and the sum.
+// Phase 3: values. Lanes own DIM/64 adjacent columns; each wave accumulates
+// its rows' weighted values, the waves are summed in LDS.
 constexpr uint32_t kAttnWaves = 8, kAttnThreads = 64 * kAttnWaves;
-constexpr uint32_t kRowsPerBlock = 1024;
+// One pass of 8 rows per wave: a block loads at most 64 K and V rows, so a
+// context is spread over many CUs (one CU's load path is the limit otherwise).
+constexpr uint32_t kRowsPerBlock = 64;
 template <int G>
-constexpr uint32_t attention_rows_per_wave() { return G <= 4 ? 16 : 8; }
+constexpr uint32_t attention_rows_per_wave() { return 8; }
 
 template <int DIM, int G>
 __global__ __launch_bounds__(kAttnThreads) void decode_attention_kernel(DecodeAttention a) {
-    constexpr uint32_t kRowsPerWave = attention_rows_per_wave<G>();
-    constexpr uint32_t kRowsPerPass = kAttnWaves * kRowsPerWave;
-    constexpr int PL = DIM / 64;   // value columns per lane
-    constexpr int KD = DIM / 16;   // key dims per lane
-    constexpr int KR = kRowsPerWave / 4;  // key rows per lane
+    constexpr uint32_t RW = attention_rows_per_wave<G>();
+    constexpr uint32_t P = kAttnWaves * RW;  // rows per pass
+    constexpr int PL = DIM / 64;             // value columns per lane
+    constexpr int KD = DIM / 16;             // key dims per lane
+    constexpr int KR = RW / 4;               // key rows per lane
     constexpr uint32_t HALF = DIM / 2;
     constexpr uint32_t rec = DIM + 2;
     extern __shared__ float smem[];
     __shared__ int is_last;
+    __shared__ float stats[G][2];  // per head: maximum, sum of exp
     const uint32_t width = a.kh * DIM;
     const uint32_t kvh = blockIdx.x, split = blockIdx.y;
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    float *qs = smem;                          // [G][DIM]
-    float *knew = qs + G * DIM;                // [DIM] rotated new key
-    float *vnew = knew + DIM;                  // [DIM]
-    float *pw = vnew + DIM;                    // [kAttnWaves][kRowsPerWave][G]
-    float *wpart = pw + kAttnWaves * kRowsPerWave * G;  // [kAttnWaves + 1][G][rec]
+    float *qs = smem;                            // [G][DIM]
+    float *knew = qs + G * DIM;                  // [DIM] rotated new key
+    float *vnew = knew + DIM;                    // [DIM]
+    float *sc = vnew + DIM;                      // [kRowsPerBlock + 1][G]
+    float *wpart = sc + (kRowsPerBlock + 1) * G; // [kAttnWaves][G][DIM]
 
     // Count-independent operands: wave g < G normalizes query head g, the last
     // wave the new key; lane j < DIM/2 holds elements j and j + DIM/2.
+    // Loaded unconditionally (lanes and waves with no use read valid data they
+    // ignore) and kept as raw bits until used, so no wait is forced here.
     const bool qwave = wave < (uint32_t)G, kwave = wave == kAttnWaves - 1;
     const bool hl = lane < HALF;
-    float qx[2] = {0.0f, 0.0f}, qw[2] = {0.0f, 0.0f};
-    float kx[2] = {0.0f, 0.0f}, kw[2] = {0.0f, 0.0f}, vx[2] = {0.0f, 0.0f};
-    if (qwave && hl) {
-        const float *x = a.qkv + (uint64_t)(kvh * G + wave) * DIM;
-        qx[0] = x[lane];
-        qx[1] = x[lane + HALF];
-        qw[0] = bf16f(a.qn[lane]);
-        qw[1] = bf16f(a.qn[lane + HALF]);
-    }
-    if (kwave && hl) {
-        const float *x = a.qkv + (uint64_t)(a.qh + kvh) * DIM;
-        const float *vs = a.qkv + (uint64_t)(a.qh + a.kh + kvh) * DIM;
-        kx[0] = x[lane];
-        kx[1] = x[lane + HALF];
-        kw[0] = bf16f(a.kn[lane]);
-        kw[1] = bf16f(a.kn[lane + HALF]);
-        vx[0] = vs[lane];
-        vx[1] = vs[lane + HALF];
-    }
+    const uint32_t hj = lane % HALF;
+    const float *qsrc = a.qkv + (uint64_t)(kvh * G + (qwave ? wave : 0)) * DIM;
+    const float *ksrc = a.qkv + (uint64_t)(a.qh + kvh) * DIM;
+    const float *vsrc = a.qkv + (uint64_t)(a.qh + a.kh + kvh) * DIM;
+    const float qx[2] = {qsrc[hj], qsrc[hj + HALF]};
+    const uint32_t qwb[2] = {a.qn[hj], a.qn[hj + HALF]};
+    const float kx[2] = {ksrc[hj], ksrc[hj + HALF]};
+    const uint32_t kwb[2] = {a.kn[hj], a.kn[hj + HALF]};
+    const float vx[2] = {vsrc[hj], vsrc[hj + HALF]};
 
     const uint32_t count = a.params->count[a.layer];
     const uint32_t n = count + 1;
@@ -1214,36 +1261,40 @@ __global__ __launch_bounds__(kAttnThreads) void decode_attention_kernel(DecodeAt
     if (split >= splits) return;
     const uint32_t per = (n + splits - 1) / splits;
     const uint32_t lo = split * per < n ? split * per : n;
-    const uint32_t hi = lo + per < n ? lo + per : n;
+    uint32_t hi = lo + per < n ? lo + per : n;
+    if (hi - lo > kRowsPerBlock) hi = lo + kRowsPerBlock;  // the host sizes splits so this never cuts
     const bool owner = count >= lo && count < hi;
     // Cached rows of this block; the appended row (index count, the last one)
-    // joins in the merge as one more partial.
+    // is scored from LDS.
     const uint32_t hr = hi < count ? hi : count;
-    float rc = 0.0f, rs = 0.0f;
-    if ((qwave || (kwave && owner)) && hl) {
-        const float *cs = a.table + (uint64_t)count * DIM;
-        rc = cs[lane];
-        rs = cs[HALF + lane];
-    }
+    const float *cs = a.table + (uint64_t)count * DIM;
+    const float rc = cs[hj], rs = cs[HALF + hj];
 
+    // Every lane loads unconditionally, also past the range (branches around
+    // loads make the compiler wait for every load in flight where paths
+    // merge); such rows are masked later. They are mirrored back into the
+    // block's rows rather than clamped to one row, which would send every
+    // such load to one memory channel.
     const float *kbase = a.k_rot + (uint64_t)kvh * DIM;
     const float *vbase = a.v + (uint64_t)kvh * DIM;
     const uint32_t kd0 = (lane & 15) * KD, rg = lane >> 4;
-    // Every lane loads unconditionally, also past the range (rows clamped to
-    // the last cached row; their scores are masked, so their weight is 0):
-    // branches around loads make the compiler wait for every load in flight
-    // where paths merge. Addresses are a wave-uniform row base plus a small
-    // lane byte offset.
-    const uint32_t last = hr > 0 ? hr - 1 : 0;
-    const uint32_t koff = (rg * width + kd0) * 4, voff = lane * PL * 4;
-    auto load_pass = [&](uint32_t base, float (&kr)[KR][KD], float (&vr)[kRowsPerWave][PL]) {
+    const uint32_t span = hr > lo ? hr - lo : 0;
+    const float inv_span = span ? 1.0f / (float)span : 0.0f;
+    auto valid_row = [&](uint32_t row) -> uint32_t {
+        if (row < hr) return row;
+        if (!span) return lo;
+        // hr - 1 - ((row - hr) mod span); the float quotient is off by at most one.
+        const int past = (int)(row - hr);
+        int r = past - (int)((float)past * inv_span) * (int)span;
+        r = r < 0 ? r + (int)span : (r >= (int)span ? r - (int)span : r);
+        return hr - 1 - (uint32_t)r;
+    };
+    const uint32_t voff = lane * PL * 4;
+    auto load_k = [&](uint32_t base, float (&kr)[KR][KD]) {
 #pragma unroll
         for (int j = 0; j < KR; ++j) {
-            // Row base + rg + 4j, clamped: the lane offset of rg is dropped
-            // when the row would pass `last`.
-            const uint32_t row = base + 4 * j;
-            const uint32_t mine = row + rg <= last ? koff : kd0 * 4;
-            const char *k = (const char *)(kbase + (uint64_t)min(row, last) * width) + mine;
+            const uint32_t row = valid_row(base + rg + 4 * j);
+            const char *k = (const char *)(kbase + (uint64_t)row * width + kd0);
 #pragma unroll
             for (int i = 0; i < KD; i += 4) {
                 f32x4 x = *(const f32x4 *)(k + 4 * i);
@@ -1253,9 +1304,11 @@ __global__ __launch_bounds__(kAttnThreads) void decode_attention_kernel(DecodeAt
                 kr[j][i + 3] = x.w;
             }
         }
+    };
+    auto load_v = [&](uint32_t base, float (&vr)[RW][PL]) {
 #pragma unroll
-        for (int r = 0; r < (int)kRowsPerWave; ++r) {
-            const char *vp = (const char *)(vbase + (uint64_t)min(base + r, last) * width) + voff;
+        for (int r = 0; r < (int)RW; ++r) {
+            const char *vp = (const char *)(vbase + (uint64_t)valid_row(base + r) * width) + voff;
             if (PL == 2) {
                 f32x2 x = *(const f32x2 *)vp;
                 vr[r][0] = x.x;
@@ -1266,41 +1319,43 @@ __global__ __launch_bounds__(kAttnThreads) void decode_attention_kernel(DecodeAt
             }
         }
     };
-    const uint32_t base0 = lo + wave * kRowsPerWave;
-    float kc0[KR][KD], vc0[kRowsPerWave][PL], kc1[KR][KD], vc1[kRowsPerWave][PL];
+    const uint32_t base0 = lo + wave * RW;
+    float kc0[KR][KD], vc0[RW][PL];
+    // K before V: the scores need K first and loads return in order.
     __builtin_amdgcn_sched_barrier(0);
-    load_pass(base0, kc0, vc0);
-    load_pass(base0 + kRowsPerPass, kc1, vc1);
+    load_k(base0, kc0);
+    __builtin_amdgcn_sched_barrier(0);
+    load_v(base0, vc0);
     __builtin_amdgcn_sched_barrier(0);
 
     // Offset-1 head RMSNorm then split-half rotation (src/qkv.s:36-67,
     // tests/rope_reference.s:14-30).
     if (qwave) {
-        float ss = qx[0] * qx[0];
-        float t = qx[1] * qx[1];
+        float ss = hl ? qx[0] * qx[0] : 0.0f;
+        float t = hl ? qx[1] * qx[1] : 0.0f;
         ss = wave_sum(ss + t);
         float ms = ss / (float)DIM;
         ms = ms + 0.000001f;
         const float inv = 1.0f / __builtin_sqrtf(ms);
         if (hl) {
-            float va = (qx[0] * inv) * (qw[0] + 1.0f);
-            float vb = (qx[1] * inv) * (qw[1] + 1.0f);
+            float va = (qx[0] * inv) * (bf16f(qwb[0]) + 1.0f);
+            float vb = (qx[1] * inv) * (bf16f(qwb[1]) + 1.0f);
             float p0 = va * rc, p1 = vb * rs, p2 = vb * rc, p3 = va * rs;
             qs[wave * DIM + lane] = p0 - p1;
             qs[wave * DIM + lane + HALF] = p2 + p3;
         }
     }
     if (kwave && owner) {
-        float ss = kx[0] * kx[0];
-        float t = kx[1] * kx[1];
+        float ss = hl ? kx[0] * kx[0] : 0.0f;
+        float t = hl ? kx[1] * kx[1] : 0.0f;
         ss = wave_sum(ss + t);
         float ms = ss / (float)DIM;
         ms = ms + 0.000001f;
         const float inv = 1.0f / __builtin_sqrtf(ms);
         if (hl) {
             const uint64_t o = (uint64_t)count * width + (uint64_t)kvh * DIM;
-            float va = (kx[0] * inv) * (kw[0] + 1.0f);
-            float vb = (kx[1] * inv) * (kw[1] + 1.0f);
+            float va = (kx[0] * inv) * (bf16f(kwb[0]) + 1.0f);
+            float vb = (kx[1] * inv) * (bf16f(kwb[1]) + 1.0f);
             float p0 = va * rc, p1 = vb * rs, p2 = vb * rc, p3 = va * rs;
             float ra = p0 - p1, rb = p2 + p3;
             knew[lane] = ra;
@@ -1326,20 +1381,11 @@ __global__ __launch_bounds__(kAttnThreads) void decode_attention_kernel(DecodeAt
     }
     __syncthreads();
 
+    // Phase 1: scores of the cached rows, then of the appended row.
     const float scale = 1.0f / __builtin_sqrtf((float)DIM);
-    float m[G], l[G], acc[G][PL];
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-        m[g] = -__builtin_inff();
-        l[g] = 0.0f;
-#pragma unroll
-        for (int e = 0; e < PL; ++e) acc[g][e] = 0.0f;
-    }
-    float *pwave = pw + wave * kRowsPerWave * G;
-    auto consume = [&](uint32_t base, float (&kc)[KR][KD], float (&vc)[kRowsPerWave][PL]) {
+    auto score = [&](uint32_t base, const float (&kc)[KR][KD]) {
 #pragma unroll
         for (int g = 0; g < G; ++g) {
-            // The query slice is read from LDS per pass, not held in registers.
             float q[KD];
 #pragma unroll
             for (int i = 0; i < KD; i += 4) {
@@ -1349,75 +1395,26 @@ __global__ __launch_bounds__(kAttnThreads) void decode_attention_kernel(DecodeAt
                 q[i + 2] = x.z;
                 q[i + 3] = x.w;
             }
-            float sc[KR];
-            float mx = -__builtin_inff();
 #pragma unroll
             for (int j = 0; j < KR; ++j) {
                 float s = 0.0f;
 #pragma unroll
                 for (int i = 0; i < KD; ++i) s = __builtin_fmaf(q[i], kc[j][i], s);
                 s = row_sum16(s);
-                const bool valid = base + rg + 4 * j < hr;
-                sc[j] = valid ? s * scale : -__builtin_inff();
-                mx = fmaxf(mx, sc[j]);
-            }
-            mx = rows_max(mx);
-            const float mn = fmaxf(m[g], mx);
-            const float corr = plamo_exp(m[g] - mn);
-            float ps = 0.0f;
-#pragma unroll
-            for (int j = 0; j < KR; ++j) {
-                // Masked rows: exp(-inf) is 0 (plamo_exp maps NaN and -inf to 0).
-                float p = plamo_exp(sc[j] - mn);
-                ps += p;
-                if ((lane & 15) == 0) pwave[(rg + 4 * j) * G + g] = p;
-            }
-            ps = rows_sum(ps);
-            l[g] = l[g] * corr + ps;
-            m[g] = mn;
-#pragma unroll
-            for (int e = 0; e < PL; ++e) acc[g][e] = acc[g][e] * corr;
-        }
-        // The weights written above are read back by every lane of this wave;
-        // LDS operations of one wave complete in order.
-        __builtin_amdgcn_wave_barrier();
-#pragma unroll
-        for (int r = 0; r < (int)kRowsPerWave; ++r) {
-#pragma unroll
-            for (int g = 0; g < G; ++g) {
-                const float pr = pwave[r * G + g];
-#pragma unroll
-                for (int e = 0; e < PL; ++e) acc[g][e] = __builtin_fmaf(pr, vc[r][e], acc[g][e]);
+                const uint32_t row = base + rg + 4 * j;
+                if ((lane & 15) == 0 && row < hr) sc[(row - lo) * G + g] = s * scale;
             }
         }
-        __builtin_amdgcn_wave_barrier();
     };
-    // The scheduling fences keep each refill after the consumption of the
-    // buffer it overwrites (otherwise the scheduler hoists it and spills).
-    for (uint32_t b = base0; b < hr; b += 2 * kRowsPerPass) {
-        consume(b, kc0, vc0);
-        __builtin_amdgcn_sched_barrier(0);
-        load_pass(b + 2 * kRowsPerPass, kc0, vc0);
-        __builtin_amdgcn_sched_barrier(0);
-        if (b + kRowsPerPass >= hr) break;
-        consume(b + kRowsPerPass, kc1, vc1);
-        __builtin_amdgcn_sched_barrier(0);
-        load_pass(b + 3 * kRowsPerPass, kc1, vc1);
-        __builtin_amdgcn_sched_barrier(0);
+    // The pass runs straight-line and unconditionally (rows past the range are
+    // masked): a loop here would merge two load histories and the compiler
+    // would then wait for every load in flight. (Blocks never hold more rows
+    // than one pass; the loop covers a caller that under-sizes the splits.)
+    score(base0, kc0);
+    for (uint32_t b = base0 + P; b < hr; b += P) {
+        load_k(b, kc0);
+        score(b, kc0);
     }
-    // Merge the waves in LDS.
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-        float *wp = wpart + (wave * G + g) * rec;
-        if (lane == 0) {
-            wp[0] = m[g];
-            wp[1] = l[g];
-        }
-#pragma unroll
-        for (int e = 0; e < PL; ++e) wp[2 + lane * PL + e] = acc[g][e];
-    }
-    // The appended row as a partial of its own: max = its score, sum = 1,
-    // accumulator = its value row.
     if (kwave && owner) {
         for (int g = 0; g < G; ++g) {
             float s = 0.0f;
@@ -1425,79 +1422,118 @@ __global__ __launch_bounds__(kAttnThreads) void decode_attention_kernel(DecodeAt
             for (int e = 0; e < PL; ++e)
                 s = __builtin_fmaf(qs[g * DIM + lane * PL + e], knew[lane * PL + e], s);
             s = wave_sum(s);
-            float *wp = wpart + (kAttnWaves * G + g) * rec;
-            if (lane == 0) {
-                wp[0] = s * scale;
-                wp[1] = 1.0f;
-            }
-#pragma unroll
-            for (int e = 0; e < PL; ++e) wp[2 + lane * PL + e] = vnew[lane * PL + e];
+            if (lane == 0) sc[(count - lo) * G + g] = s * scale;
         }
     }
     __syncthreads();
-    const uint32_t parts = kAttnWaves + (owner ? 1 : 0);
+
+    // Phase 2: per head, the maximum over the block's rows, exp in place, sum.
+    const uint32_t rows = (owner ? count + 1 : hr) - lo;
+    if (qwave) {
+        const uint32_t g = wave;
+        float mx = -__builtin_inff();
+        for (uint32_t r = lane; r < rows; r += 64) mx = fmaxf(mx, sc[r * G + g]);
+        mx = wave_max(mx);
+        float sum = 0.0f;
+        for (uint32_t r = lane; r < rows; r += 64) {
+            const float p = plamo_exp(sc[r * G + g] - mx);
+            sc[r * G + g] = p;
+            sum += p;
+        }
+        sum = wave_sum(sum);
+        if (lane == 0) {
+            stats[g][0] = mx;
+            stats[g][1] = sum;
+        }
+    }
+    __syncthreads();
+
+    // Phase 3: weighted values.
+    float acc[G][PL];
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+        for (int e = 0; e < PL; ++e) acc[g][e] = 0.0f;
+    auto accumulate = [&](uint32_t base, const float (&vc)[RW][PL]) {
+#pragma unroll
+        for (int r = 0; r < (int)RW; ++r) {
+            const uint32_t row = base + r;
+            float pr[G];
+            if (G % 4 == 0) {
+#pragma unroll
+                for (int g = 0; g < G; g += 4) {
+                    f32x4 x = *(const f32x4 *)(sc + (row - lo) * G + g);
+                    pr[g] = x.x;
+                    pr[g + 1] = x.y;
+                    pr[g + 2] = x.z;
+                    pr[g + 3] = x.w;
+                }
+            } else {
+#pragma unroll
+                for (int g = 0; g < G; ++g) pr[g] = sc[(row - lo) * G + g];
+            }
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+                const float p = row < hr ? pr[g] : 0.0f;
+#pragma unroll
+                for (int e = 0; e < PL; ++e) acc[g][e] = __builtin_fmaf(p, vc[r][e], acc[g][e]);
+            }
+        }
+    };
+    accumulate(base0, vc0);
+    for (uint32_t b = base0 + P; b < hr; b += P) {
+        load_v(b, vc0);
+        accumulate(b, vc0);
+    }
+    if (kwave && owner) {
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            const float p = sc[(count - lo) * G + g];
+#pragma unroll
+            for (int e = 0; e < PL; ++e)
+                acc[g][e] = __builtin_fmaf(p, vnew[lane * PL + e], acc[g][e]);
+        }
+    }
+    // Sum the waves in LDS.
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+        for (int e = 0; e < PL; ++e) wpart[(wave * G + g) * DIM + lane * PL + e] = acc[g][e];
+    __syncthreads();
     for (uint32_t i = threadIdx.x; i < G * DIM; i += kAttnThreads) {
         const uint32_t g = i / DIM, d = i % DIM;
-        float mx = -__builtin_inff();
-        for (uint32_t w = 0; w < parts; ++w) mx = fmaxf(mx, wpart[(w * G + g) * rec]);
-        float sum = 0.0f, o = 0.0f;
-        for (uint32_t w = 0; w < parts; ++w) {
-            const float *wp = wpart + (w * G + g) * rec;
-            const float f = wp[0] == -__builtin_inff() ? 0.0f : plamo_exp(wp[0] - mx);
-            sum = __builtin_fmaf(wp[1], f, sum);
-            o = __builtin_fmaf(wp[2 + d], f, o);
-        }
+        float o = 0.0f;
+#pragma unroll
+        for (uint32_t w = 0; w < kAttnWaves; ++w) o = o + wpart[(w * G + g) * DIM + d];
         if (splits == 1) {
-            a.out[(uint64_t)(kvh * G + g) * DIM + d] = o / sum;
+            a.out[(uint64_t)(kvh * G + g) * DIM + d] = o / stats[g][1];
         } else {
             float *bp = a.partial + ((uint64_t)(kvh * a.splits + split) * G + g) * rec;
             if (d == 0) {
-                bp[0] = mx;
-                bp[1] = sum;
+                store_through(bp, stats[g][0]);
+                store_through(bp + 1, stats[g][1]);
             }
-            bp[2 + d] = o;
+            store_through(bp + 2 + d, o);
         }
     }
     if (splits == 1) return;
-    // Release the partial at device scope (other XCDs' L2 included), count the
-    // block; the last block of this KV head acquires and merges.
-    __threadfence();
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        uint32_t done = atomicAdd(&a.counters[kvh], 1u);
-        is_last = done + 1 == splits;
-    }
-    __syncthreads();
-    if (!is_last) return;
-    __threadfence();
+    // The last block of this KV head merges the partials.
+    if (!arrive_last(&a.counters[kvh], splits, &is_last)) return;
     for (uint32_t i = threadIdx.x; i < G * DIM; i += kAttnThreads) {
         const uint32_t g = i / DIM, d = i % DIM;
-        float ms[8], ls[8], os[8];
-#pragma unroll
-        for (int sI = 0; sI < 8; ++sI) {
-            ms[sI] = -__builtin_inff();
-            ls[sI] = 0.0f;
-            os[sI] = 0.0f;
-            if (sI < (int)splits) {
-                const float *bp = a.partial + ((uint64_t)(kvh * a.splits + sI) * G + g) * rec;
-                ms[sI] = bp[0];
-                ls[sI] = bp[1];
-                os[sI] = bp[2 + d];
-            }
-        }
+        const float *bp = a.partial + ((uint64_t)kvh * a.splits * G + g) * rec;
         float mx = -__builtin_inff();
-#pragma unroll
-        for (int sI = 0; sI < 8; ++sI) mx = fmaxf(mx, ms[sI]);
+        for (uint32_t sI = 0; sI < splits; ++sI)
+            mx = fmaxf(mx, load_through(bp + (uint64_t)sI * G * rec));
         float sum = 0.0f, o = 0.0f;
-#pragma unroll
-        for (int sI = 0; sI < 8; ++sI) {
-            float f = ms[sI] == -__builtin_inff() ? 0.0f : plamo_exp(ms[sI] - mx);
-            sum = __builtin_fmaf(ls[sI], f, sum);
-            o = __builtin_fmaf(os[sI], f, o);
+        for (uint32_t sI = 0; sI < splits; ++sI) {
+            const float *q = bp + (uint64_t)sI * G * rec;
+            const float f = plamo_exp(load_through(q) - mx);
+            sum = __builtin_fmaf(load_through(q + 1), f, sum);
+            o = __builtin_fmaf(load_through(q + 2 + d), f, o);
         }
         a.out[(uint64_t)(kvh * G + g) * DIM + d] = o / sum;
     }
-    if (threadIdx.x == 0) a.counters[kvh] = 0;
 }
 
 bool decode_attention_supported(uint32_t dim, uint32_t group) {
@@ -1505,10 +1541,12 @@ bool decode_attention_supported(uint32_t dim, uint32_t group) {
            (group == 1 || group == 2 || group == 4 || group == 6 || group == 8);
 }
 
+uint32_t decode_attention_splits(uint64_t rows) {
+    return (uint32_t)((rows + kRowsPerBlock - 1) / kRowsPerBlock);
+}
+
 static size_t decode_attention_lds(uint32_t dim, uint32_t group) {
-    const uint32_t rows = group <= 4 ? 16 : 8;
-    return (group * dim + 2 * dim + kAttnWaves * rows * group +
-            (kAttnWaves + 1) * group * (dim + 2)) *
+    return (group * dim + 2 * dim + (kRowsPerBlock + 1) * group + kAttnWaves * group * dim) *
            sizeof(float);
 }
 
@@ -1536,7 +1574,7 @@ static hipError_t decode_attention_dim(hipStream_t stream, const DecodeAttention
 }
 
 hipError_t launch_decode_attention(hipStream_t stream, const DecodeAttention &a) {
-    if (!decode_attention_supported(a.dim, a.qh / a.kh) || a.splits < 1 || a.splits > 8)
+    if (!decode_attention_supported(a.dim, a.qh / a.kh) || a.splits < 1 || a.splits > 65535)
         return hipErrorInvalidValue;
     return a.dim == 64 ? decode_attention_dim<64>(stream, a) : decode_attention_dim<128>(stream, a);
 }
