@@ -62,6 +62,7 @@ struct Layer {
     bool fused = false;  // decode attention fused with the Q/K norm and KV append
     uint32_t rope = 0;
     float *k = nullptr, *v = nullptr, *rot = nullptr;
+    float *host_k = nullptr, *host_v = nullptr, *host_rot = nullptr;  // device views of pinned host rows
     uint64_t rows = 0;          // device rows allocated
     // Shadow of the host bookkeeping after this backend's last return.
     bool synced = false;
@@ -104,6 +105,10 @@ struct plamo_metal {
     uint32_t *counters = nullptr;
     float *outbox = nullptr, *outbox_host = nullptr;  // logits | state | normalized | stage
     uint64_t outbox_floats = 0;
+    // When every host array a step updates is pinned and device-visible, the
+    // graph writes them in place (no host-side mirror copies).
+    bool host_direct = false;
+    float *host_state = nullptr, *host_norm = nullptr;
     // Prompt / candidate workspace (grown on demand).
     uint64_t prompt_rows = 0;
     Buffer p_state, p_norm, p_qkv, p_q, p_attn, p_branch, p_gu, p_act, p_side_k, p_side_v,
@@ -324,6 +329,32 @@ int ensure_kv_rows(plamo_metal *m, Layer &l, uint64_t rows) {
     return 1;
 }
 
+// Device address of pinned host memory, or nullptr for pageable memory.
+float *device_view(void *p) {
+    hipPointerAttribute_t attr{};
+    if (!p || hipPointerGetAttributes(&attr, p) != hipSuccess) {
+        (void)hipGetLastError();
+        return nullptr;
+    }
+    if (attr.type != hipMemoryTypeHost || !attr.devicePointer) return nullptr;
+    return (float *)attr.devicePointer;
+}
+
+void find_host_views(plamo_metal *m, struct model *model) {
+    m->host_state = device_view(model->state);
+    m->host_norm = device_view(model->normalized);
+    bool ok = m->host_state && m->host_norm && device_view(model->logits);
+    for (uint64_t i = 0; i < model->count; ++i) {
+        Layer &d = m->layers[i];
+        struct mixer *mx = model->layers[i]->mixer;
+        d.host_k = device_view(mx->cache->k);
+        d.host_v = device_view(mx->cache->v);
+        d.host_rot = device_view(mx->rotation->out);
+        ok = ok && d.host_k && d.host_v && d.host_rot;
+    }
+    m->host_direct = ok;
+}
+
 int prepare(plamo_metal *m, struct model *model) {
     if (m->model == model) return 1;
     release_model(m);
@@ -484,6 +515,7 @@ int prepare(plamo_metal *m, struct model *model) {
         return problem(m, "cannot allocate decode workspace");
     }
     m->model = model;
+    find_host_views(m, model);
     ++m->epoch;
     return 1;
 }
@@ -571,6 +603,7 @@ int end_timing(plamo_metal *m) {
 struct DecodePlan {
     std::vector<char> stale, shift;
     bool special = false;
+    bool direct = false;  // host arrays written in place by the step itself
 };
 
 // Enqueues one decode step: embedding, every layer, final norm + head, and the
@@ -622,7 +655,12 @@ int encode_decode(plamo_metal *m, struct model *model, const DecodePlan &plan, i
             da.k_raw = d.k;
             da.v = d.v;
             da.k_rot = d.rot;
-            da.stage = layer_stage;
+            da.stage = plan.direct ? nullptr : layer_stage;
+            if (plan.direct) {
+                da.host_k = d.host_k;
+                da.host_v = d.host_v;
+                da.host_rot = d.host_rot;
+            }
             da.out = m->attn;
             da.partial = m->partial;
             da.counters = m->counters;
@@ -714,12 +752,15 @@ int encode_decode(plamo_metal *m, struct model *model, const DecodePlan &plan, i
     ph.branch = m->down_out;
     ph.rw = m->layers[L - 1].norms + 3 * h;
     ph.roffset = kMlpOffset;
-    ph.state_out = state_out;
-    ph.norm_out = norm_out;
+    ph.state_out = plan.direct ? m->host_state : state_out;
+    ph.norm_out = plan.direct ? m->host_norm : norm_out;
     HIP_TRY(m, launch_gemv(s, m->head, V, h, ph, logits, 0, blocks));
     ++n;
-    HIP_TRY(m, hipMemcpyAsync(m->outbox_host, m->outbox, m->outbox_floats * 4,
-                              hipMemcpyDeviceToHost, s));
+    if (plan.direct)
+        HIP_TRY(m, hipMemcpyAsync(model->logits, logits, V * 4, hipMemcpyDeviceToHost, s));
+    else
+        HIP_TRY(m, hipMemcpyAsync(m->outbox_host, m->outbox, m->outbox_floats * 4,
+                                  hipMemcpyDeviceToHost, s));
     *dispatches = n;
     return 1;
 }
@@ -969,6 +1010,7 @@ int plamo_metal_forward(struct plamo_metal *m, struct model *model, uint64_t tok
     if (plan.special && (!ensure_prompt(m, model, 1) || !ensure_window_scratch(m, model))) return -1;
     m->params_host->token = (uint32_t)token;
     m->params_host->tokens = 1;
+    plan.direct = m->host_direct && !plan.special;
     int dispatches = 0;
     begin_timing(m);
     if (plan.special) {
@@ -1000,11 +1042,14 @@ int plamo_metal_forward(struct plamo_metal *m, struct model *model, uint64_t tok
     }
     if (!end_timing(m)) return fail(m);
     m->info.dispatches += dispatches;
-    // Host mirror (runtime/metal_model.m:491-500).
+    // Host mirror (runtime/metal_model.m:491-500); a direct step has written
+    // logits, state, normalized and the new rows in place already.
     const float *out = m->outbox_host;
-    memcpy(model->logits, out, V * 4);
-    memcpy(model->state, out + V, h * 4);
-    memcpy(model->normalized, out + V + h, h * 4);
+    if (!plan.direct) {
+        memcpy(model->logits, out, V * 4);
+        memcpy(model->state, out + V, h * 4);
+        memcpy(model->normalized, out + V + h, h * 4);
+    }
     const float *stage = out + V + 2 * h;
     for (uint64_t i = 0; i < L; ++i) {
         Layer &d = m->layers[i];
@@ -1018,15 +1063,17 @@ int plamo_metal_forward(struct plamo_metal *m, struct model *model, uint64_t tok
             memmove(c->v, c->v + c->width, (c->capacity - 1) * c->width * 4);
             row = c->capacity - 1;
         }
-        memcpy(c->k + row * c->width, st, c->width * 4);
-        memcpy(c->v + row * c->width, st + c->width, c->width * 4);
+        if (!plan.direct) {
+            memcpy(c->k + row * c->width, st, c->width * 4);
+            memcpy(c->v + row * c->width, st + c->width, c->width * 4);
+        }
         uint64_t count = row + 1;
         if (plan.shift[i] || plan.stale[i]) {
             if (hipMemcpy(r->out, d.rot, count * c->width * 4, hipMemcpyDeviceToHost) != hipSuccess) {
                 problem(m, "cannot mirror rotated keys");
                 return fail(m);
             }
-        } else {
+        } else if (!plan.direct) {
             memcpy(r->out + row * c->width, st + 2 * c->width, c->width * 4);
         }
         c->count = count;

@@ -9,6 +9,7 @@
  * call fails. This file computes nothing on the model.
  */
 #include "../../include/plamo_compute.h"
+#include <emmintrin.h>
 #include <math.h>
 #include <string.h>
 
@@ -51,18 +52,48 @@ int plamo_prefill(struct model *model, const uint32_t *ids, uint64_t tokens, flo
     return cpu_path.prefill ? cpu_path.prefill(model, ids, tokens, states) : 0;
 }
 
+/* src/token.s:37-63: index of the first maximal element (strict >), any NaN
+ * gives UINT64_MAX. Two SSE2 passes: the maximum with a NaN check, then the
+ * first element equal to it (equivalent to the strict sequential scan: equal
+ * values never replace the first one). */
 uint64_t plamo_argmax(const float *x, uint64_t n) {
-    if (!n || isnan(x[0]))
+    if (!n)
         return UINT64_MAX;
-    uint64_t best = 0;
-    float value = x[0];
-    for (uint64_t i = 1; i < n; ++i) {
+    __m128 m0 = _mm_set1_ps(x[0]), m1 = m0, m2 = m0, m3 = m0;
+    __m128 unordered = _mm_setzero_ps();
+    uint64_t i = 0;
+    for (; i + 16 <= n; i += 16) {
+        const __m128 a = _mm_loadu_ps(x + i), b = _mm_loadu_ps(x + i + 4);
+        const __m128 c = _mm_loadu_ps(x + i + 8), d = _mm_loadu_ps(x + i + 12);
+        unordered = _mm_or_ps(unordered, _mm_or_ps(_mm_cmpunord_ps(a, b), _mm_cmpunord_ps(c, d)));
+        m0 = _mm_max_ps(m0, a);
+        m1 = _mm_max_ps(m1, b);
+        m2 = _mm_max_ps(m2, c);
+        m3 = _mm_max_ps(m3, d);
+    }
+    if (_mm_movemask_ps(unordered))
+        return UINT64_MAX;
+    __m128 m = _mm_max_ps(_mm_max_ps(m0, m1), _mm_max_ps(m2, m3));
+    m = _mm_max_ps(m, _mm_shuffle_ps(m, m, _MM_SHUFFLE(1, 0, 3, 2)));
+    m = _mm_max_ps(m, _mm_shuffle_ps(m, m, _MM_SHUFFLE(2, 3, 0, 1)));
+    float value = _mm_cvtss_f32(m);
+    for (; i < n; ++i) {
         if (isnan(x[i]))
             return UINT64_MAX;
-        if (x[i] > value) {
+        if (x[i] > value)
             value = x[i];
-            best = i;
-        }
     }
-    return best;
+    const __m128 v = _mm_set1_ps(value);
+    for (i = 0; i + 16 <= n; i += 16) {
+        const int hit = _mm_movemask_ps(_mm_cmpeq_ps(_mm_loadu_ps(x + i), v)) |
+                        _mm_movemask_ps(_mm_cmpeq_ps(_mm_loadu_ps(x + i + 4), v)) << 4 |
+                        _mm_movemask_ps(_mm_cmpeq_ps(_mm_loadu_ps(x + i + 8), v)) << 8 |
+                        _mm_movemask_ps(_mm_cmpeq_ps(_mm_loadu_ps(x + i + 12), v)) << 12;
+        if (hit)
+            return i + (uint64_t)__builtin_ctz((unsigned)hit);
+    }
+    for (; i < n; ++i)
+        if (x[i] == value)
+            return i;
+    return UINT64_MAX; /* unreachable: the maximum is one of the elements */
 }

@@ -113,6 +113,7 @@ struct DecodeAttention {
     const float *table;      // RoPE rows [position][dim]: cos | sin
     float *k_raw, *v, *k_rot;  // cache rows [rows, kh*dim]
     float *stage;            // optional [3][kh*dim] copy of the appended row
+    float *host_k, *host_v, *host_rot;  // optional device views of the host cache rows
     float *out;              // [qh*dim]
     float *partial;          // scratch [kh][splits][qh/kh][dim + 2]
     uint32_t *counters;      // [kh] zero-initialized; reset by the kernel

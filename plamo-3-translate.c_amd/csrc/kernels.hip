@@ -1377,6 +1377,14 @@ __global__ __launch_bounds__(kAttnThreads) void decode_attention_kernel(DecodeAt
                 st[2 * width + lane] = ra;
                 st[2 * width + lane + HALF] = rb;
             }
+            if (a.host_k) {
+                a.host_k[o + lane] = va;
+                a.host_k[o + lane + HALF] = vb;
+                a.host_v[o + lane] = vx[0];
+                a.host_v[o + lane + HALF] = vx[1];
+                a.host_rot[o + lane] = ra;
+                a.host_rot[o + lane + HALF] = rb;
+            }
         }
     }
     __syncthreads();

@@ -33,11 +33,14 @@ SHAPES = [  # (hidden, intermediate, head_dim, global capacity) of tests/metal_d
 ]
 
 
+@pytest.mark.parametrize("pinned", [False, True])
 @pytest.mark.parametrize("h,inter,dim,capacity", SHAPES)
-def test_decode_steps(h, inter, dim, capacity):
-    say(f"decode h={h} I={inter} dim={dim} cap={capacity}")
+def test_decode_steps(h, inter, dim, capacity, pinned):
+    # pinned: host arrays the decode graph writes in place (shift and stale
+    # steps still take the eager path with host mirror copies).
+    say(f"decode h={h} I={inter} dim={dim} cap={capacity} pinned={pinned}")
     s = tiny(h=h, inter=inter, dim=dim, capacity=capacity)
-    a, b = s.instance(), s.instance()
+    a, b = s.instance(pinned=pinned), s.instance()
     be = plamo_hip.Backend(s)
     try:
         steps = min(capacity, 140)

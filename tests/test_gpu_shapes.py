@@ -24,8 +24,8 @@ def threads():
     oracle_lib.load().oracle_set_threads(16)
 
 
-def run_pair(syn, steps, prompt, fill=0):
-    gpu, cpu = syn.instance(), syn.instance()
+def run_pair(syn, steps, prompt, fill=0, pinned=False):
+    gpu, cpu = syn.instance(pinned=pinned), syn.instance()
     be = plamo_hip.Backend(syn)
     try:
         if fill:
@@ -61,10 +61,13 @@ def test_c1_single_layer_prefilled_kv():
 
 
 def test_c4_shapes_four_layers():
+    # Pinned host arrays: the decode graph writes logits, state, normalized
+    # state and the new K/V rows into them in place (the bench's setup).
     cfg = dict(plamo_hip.CONFIGS["c4"], layers=4, vocab=1000)
     syn = plamo_hip.Synthetic(**cfg, pattern=4, seed=202)
     try:
-        run_pair(syn, steps=4, prompt=list(range(5, 5 + 69 * 7, 7)))
+        run_pair(syn, steps=4, prompt=list(range(5, 5 + 69 * 7, 7)), pinned=True)
+        run_pair(syn, steps=2, prompt=list(range(3, 3 + 20 * 5, 5)))
     finally:
         syn.close()
 
