@@ -646,6 +646,7 @@ int encode_decode(plamo_metal *m, struct model *model, const DecodePlan &plan, i
             ++n;
         }
         float *layer_stage = stage + i * 3 * m->max_width;
+        bool fused_o = false;
         if (!shift && d.fused) {
             DecodeAttention da{};
             da.qkv = m->qkv;
@@ -670,7 +671,23 @@ int encode_decode(plamo_metal *m, struct model *model, const DecodePlan &plan, i
             da.kh = d.kh;
             da.dim = d.dim;
             da.splits = decode_attention_splits(d.rows);
-            HIP_TRY(m, launch_decode_attention(s, da));
+            if (attention_o_supported(d.dim, d.qh / d.kh, (uint64_t)d.qh * d.dim) &&
+                !((uintptr_t)d.o & 15)) {
+                AttentionO ao{};
+                ao.a = da;
+                ao.w = d.o;
+                ao.x = m->attn;
+                ao.y = m->branch;
+                ao.rows = (uint32_t)h;
+                ao.cols = d.qh * d.dim;
+                ao.heads = d.kh;
+                ao.done = m->params_dev->done + i;
+                ao.error = &m->params_dev->error;
+                HIP_TRY(m, launch_attention_o(s, ao));
+                fused_o = true;
+            } else {
+                HIP_TRY(m, launch_decode_attention(s, da));
+            }
             ++n;
         } else {
             // General path (eager only: its arguments depend on the row count).
@@ -726,9 +743,11 @@ int encode_decode(plamo_metal *m, struct model *model, const DecodePlan &plan, i
                 n += 2;
             }
         }
-        Prologue po{};
-        po.src = m->attn;
-        HIP_TRY(m, launch_gemv(s, d.o, h, (uint64_t)d.qh * d.dim, po, m->branch, 0, blocks));
+        if (!fused_o) {
+            Prologue po{};
+            po.src = m->attn;
+            HIP_TRY(m, launch_gemv(s, d.o, h, (uint64_t)d.qh * d.dim, po, m->branch, 0, blocks));
+        }
         Prologue pg{};
         pg.src = cur;
         pg.w = mpre;

@@ -17,6 +17,8 @@ struct StepParams {
     uint32_t token;             // decode token id
     uint32_t tokens;            // prompt / candidate rows of this call
     uint32_t count[kMaxLayers]; // cache rows of each layer before this call
+    uint32_t done[kMaxLayers];  // fused attention: finished KV heads (zero at launch)
+    uint32_t error;             // fused attention: a wait gave up
 };
 
 // Norm applied in a GEMV prologue: x = rms(src) * (bf16(w) + offset).
@@ -122,6 +124,20 @@ struct DecodeAttention {
 };
 hipError_t launch_decode_attention(hipStream_t, const DecodeAttention &);
 bool decode_attention_supported(uint32_t dim, uint32_t group);
+// Decode attention fused with the output projection y = W_o . attention
+// (rows = hidden, cols = qh * dim). `done` must be zero at launch and counts
+// the finished KV heads; x is the attention output (a.out).
+struct AttentionO {
+    DecodeAttention a;
+    const uint16_t *w;
+    const float *x;
+    float *y;
+    uint32_t rows, cols, heads;
+    uint32_t *done;
+    uint32_t *error;
+};
+hipError_t launch_attention_o(hipStream_t, const AttentionO &);
+bool attention_o_supported(uint32_t dim, uint32_t group, uint64_t cols);
 // Blocks per KV head that cover `rows` cache rows (DecodeAttention::splits
 // must be at least this for the largest row count of the launch).
 uint32_t decode_attention_splits(uint64_t rows);

@@ -1217,8 +1217,12 @@ constexpr uint32_t kRowsPerBlock = 64;
 template <int G>
 constexpr uint32_t attention_rows_per_wave() { return 8; }
 
+// One attention block (KV head kvh, row split `split`). With `done`, the block
+// that completes a KV head's output writes it through to the coherence point
+// and counts the head in *done (the fused O projection waits on it).
 template <int DIM, int G>
-__global__ __launch_bounds__(kAttnThreads) void decode_attention_kernel(DecodeAttention a) {
+__device__ __forceinline__ void attention_block(const DecodeAttention &a, uint32_t kvh,
+                                                uint32_t split, uint32_t *done) {
     constexpr uint32_t RW = attention_rows_per_wave<G>();
     constexpr uint32_t P = kAttnWaves * RW;  // rows per pass
     constexpr int PL = DIM / 64;             // value columns per lane
@@ -1230,7 +1234,6 @@ __global__ __launch_bounds__(kAttnThreads) void decode_attention_kernel(DecodeAt
     __shared__ int is_last;
     __shared__ float stats[G][2];  // per head: maximum, sum of exp
     const uint32_t width = a.kh * DIM;
-    const uint32_t kvh = blockIdx.x, split = blockIdx.y;
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     float *qs = smem;                            // [G][DIM]
     float *knew = qs + G * DIM;                  // [DIM] rotated new key
@@ -1514,7 +1517,11 @@ __global__ __launch_bounds__(kAttnThreads) void decode_attention_kernel(DecodeAt
 #pragma unroll
         for (uint32_t w = 0; w < kAttnWaves; ++w) o = o + wpart[(w * G + g) * DIM + d];
         if (splits == 1) {
-            a.out[(uint64_t)(kvh * G + g) * DIM + d] = o / stats[g][1];
+            const float r = o / stats[g][1];
+            if (done)
+                store_through(a.out + (uint64_t)(kvh * G + g) * DIM + d, r);
+            else
+                a.out[(uint64_t)(kvh * G + g) * DIM + d] = r;
         } else {
             float *bp = a.partial + ((uint64_t)(kvh * a.splits + split) * G + g) * rec;
             if (d == 0) {
@@ -1524,7 +1531,10 @@ __global__ __launch_bounds__(kAttnThreads) void decode_attention_kernel(DecodeAt
             store_through(bp + 2 + d, o);
         }
     }
-    if (splits == 1) return;
+    if (splits == 1) {
+        if (done) arrive_last(done, 0xffffffffu, &is_last);
+        return;
+    }
     // The last block of this KV head merges the partials.
     if (!arrive_last(&a.counters[kvh], splits, &is_last)) return;
     for (uint32_t i = threadIdx.x; i < G * DIM; i += kAttnThreads) {
@@ -1540,8 +1550,82 @@ __global__ __launch_bounds__(kAttnThreads) void decode_attention_kernel(DecodeAt
             sum = __builtin_fmaf(load_through(q + 1), f, sum);
             o = __builtin_fmaf(load_through(q + 2 + d), f, o);
         }
-        a.out[(uint64_t)(kvh * G + g) * DIM + d] = o / sum;
+        if (done)
+            store_through(a.out + (uint64_t)(kvh * G + g) * DIM + d, o / sum);
+        else
+            a.out[(uint64_t)(kvh * G + g) * DIM + d] = o / sum;
     }
+    if (done) arrive_last(done, 0xffffffffu, &is_last);
+}
+
+template <int DIM, int G>
+__global__ __launch_bounds__(kAttnThreads) void decode_attention_kernel(DecodeAttention a) {
+    attention_block<DIM, G>(a, blockIdx.x, blockIdx.y, nullptr);
+}
+
+// Attention fused with the output projection (src/mixer.s:60-80: O = W_o .
+// attention). Blocks [0, kh * splits) run attention (block b: KV head
+// b % kh, split b / kh); the rest compute O rows. An O block streams its
+// weight rows into registers first, then waits until every KV head's output
+// is counted in `done` (the attention blocks have lower indices, so they are
+// dispatched first and never wait), reads the attention output and finishes
+// its dot products: the O weights cross HBM while attention runs. The wait is
+// bounded; a block that gives up writes NaN rows (they surface as a failed
+// argmax) and sets *error.
+template <int KC>
+__device__ __forceinline__ void oproj_block(const AttentionO &f, uint32_t ob) {
+    constexpr int U = 2;  // rows per wave
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t r0 = (ob * kAttnWaves + wave) * U;
+    if (r0 >= f.rows) return;
+    u32x4 wv[U][KC];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const uint32_t r = min(r0 + u, f.rows - 1);
+        const u32x4 *p = (const u32x4 *)(f.w + (uint64_t)r * f.cols + lane * 8);
+#pragma unroll
+        for (int c = 0; c < KC; ++c) wv[u][c] = __builtin_nontemporal_load(p + c * 64);
+    }
+    uint32_t spins = 0;
+    bool ok = true;
+    while (__hip_atomic_load(f.done, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < f.heads) {
+        __builtin_amdgcn_s_sleep(2);
+        if (++spins == (1u << 22)) {
+            ok = false;
+            break;
+        }
+    }
+    float acc[U] = {0.0f, 0.0f};
+#pragma unroll
+    for (int c = 0; c < KC; ++c) {
+        const f32x4 *xp = (const f32x4 *)(f.x + c * 512 + lane * 8);
+        const f32x4 x0 = xp[0], x1 = xp[1];
+        const float x[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const uint32_t q[4] = {wv[u][c].x, wv[u][c].y, wv[u][c].z, wv[u][c].w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                acc[u] = __builtin_fmaf(bf16f(q[e] & 0xffffu), x[2 * e], acc[u]);
+                acc[u] = __builtin_fmaf(__uint_as_float(q[e] & 0xffff0000u), x[2 * e + 1], acc[u]);
+            }
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const float v = wave_sum(acc[u]);
+        if (lane == 0 && r0 + u < f.rows) f.y[r0 + u] = ok ? v : __builtin_nanf("");
+    }
+    if (!ok && lane == 0) atomicOr(f.error, 1u);
+}
+
+template <int DIM, int G, int KC>
+__global__ __launch_bounds__(kAttnThreads) void attention_o_kernel(AttentionO f) {
+    const uint32_t attention_blocks = f.a.kh * f.a.splits;
+    if (blockIdx.x < attention_blocks)
+        attention_block<DIM, G>(f.a, blockIdx.x % f.a.kh, blockIdx.x / f.a.kh, f.done);
+    else
+        oproj_block<KC>(f, blockIdx.x - attention_blocks);
 }
 
 bool decode_attention_supported(uint32_t dim, uint32_t group) {
@@ -1579,6 +1663,53 @@ static hipError_t decode_attention_dim(hipStream_t stream, const DecodeAttention
     case 6: return decode_attention_variant<DIM, 6>(stream, a);
     default: return decode_attention_variant<DIM, 8>(stream, a);
     }
+}
+
+template <int DIM, int G, int KC>
+static hipError_t attention_o_variant(hipStream_t stream, const AttentionO &f) {
+    size_t lds = decode_attention_lds(DIM, G);
+    if (lds > 65536) {
+        hipError_t e = hipFuncSetAttribute((const void *)attention_o_kernel<DIM, G, KC>,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) return e;
+    }
+    const uint32_t oblocks = (f.rows + 2 * kAttnWaves - 1) / (2 * kAttnWaves);
+    attention_o_kernel<DIM, G, KC>
+        <<<f.a.kh * f.a.splits + oblocks, kAttnThreads, lds, stream>>>(f);
+    return hipGetLastError();
+}
+
+template <int DIM, int G>
+static hipError_t attention_o_cols(hipStream_t stream, const AttentionO &f) {
+    switch (f.cols / 512) {
+    case 4: return attention_o_variant<DIM, G, 4>(stream, f);
+    case 8: return attention_o_variant<DIM, G, 8>(stream, f);
+    default: return attention_o_variant<DIM, G, 12>(stream, f);
+    }
+}
+
+template <int DIM>
+static hipError_t attention_o_dim(hipStream_t stream, const AttentionO &f) {
+    switch (f.a.qh / f.a.kh) {
+    case 1: return attention_o_cols<DIM, 1>(stream, f);
+    case 2: return attention_o_cols<DIM, 2>(stream, f);
+    case 4: return attention_o_cols<DIM, 4>(stream, f);
+    case 6: return attention_o_cols<DIM, 6>(stream, f);
+    default: return attention_o_cols<DIM, 8>(stream, f);
+    }
+}
+
+bool attention_o_supported(uint32_t dim, uint32_t group, uint64_t cols) {
+    return decode_attention_supported(dim, group) &&
+           (cols == 2048 || cols == 4096 || cols == 6144);
+}
+
+hipError_t launch_attention_o(hipStream_t stream, const AttentionO &f) {
+    if (!attention_o_supported(f.a.dim, f.a.qh / f.a.kh, f.cols) || f.cols != f.a.qh * f.a.dim ||
+        f.a.splits < 1 || f.a.splits > 65535 || !f.done || !f.error || f.heads != f.a.kh ||
+        ((uintptr_t)f.w & 15) || ((uintptr_t)f.x & 15))
+        return hipErrorInvalidValue;
+    return f.a.dim == 64 ? attention_o_dim<64>(stream, f) : attention_o_dim<128>(stream, f);
 }
 
 hipError_t launch_decode_attention(hipStream_t stream, const DecodeAttention &a) {
