@@ -103,12 +103,18 @@ struct plamo_metal {
     float *state_a = nullptr, *state_b = nullptr, *qkv = nullptr, *q = nullptr, *attn = nullptr,
           *branch = nullptr, *act = nullptr, *down_out = nullptr, *partial = nullptr;
     uint32_t *counters = nullptr;
+    uint32_t *layer_counters = nullptr;  // one-launch layers: kLayerCounterWords per layer
     float *outbox = nullptr, *outbox_host = nullptr;  // logits | state | normalized | stage
     uint64_t outbox_floats = 0;
     // When every host array a step updates is pinned and device-visible, the
     // graph writes them in place (no host-side mirror copies).
     bool host_direct = false;
     float *host_state = nullptr, *host_norm = nullptr;
+    // PLAMO_HIP_LAYER_LAUNCH=1: each decode layer as one phase-chained launch
+    // where the shapes allow. Off by default: on MI355X at C4 the in-launch
+    // phase barriers cost as much as launch boundaries, and blocks waiting at
+    // a barrier hold the CU slots the next phase would prefetch into.
+    bool layer_launch = false;
     // Prompt / candidate workspace (grown on demand).
     uint64_t prompt_rows = 0;
     Buffer p_state, p_norm, p_qkv, p_q, p_attn, p_branch, p_gu, p_act, p_side_k, p_side_v,
@@ -490,6 +496,7 @@ int prepare(plamo_metal *m, struct model *model) {
     dev_free(m, m->down_out);
     dev_free(m, m->partial);
     dev_free(m, m->counters);
+    dev_free(m, m->layer_counters);
     dev_free(m, m->outbox);
     if (m->outbox_host) (void)hipHostFree(m->outbox_host);
     m->outbox_host = nullptr;
@@ -503,13 +510,15 @@ int prepare(plamo_metal *m, struct model *model) {
     m->down_out = dev_alloc<float>(m, h);
     m->partial = dev_alloc<float>(m, m->max_partial * m->max_splits);
     m->counters = dev_alloc<uint32_t>(m, 256);
+    m->layer_counters = dev_alloc<uint32_t>(m, L * kLayerCounterWords);
     m->outbox_floats = V + 2 * h + L * 3 * m->max_width;
     m->outbox = dev_alloc<float>(m, m->outbox_floats);
     if (!m->state_a || !m->state_b || !m->qkv || !m->q || !m->attn || !m->branch || !m->act ||
-        !m->down_out || !m->partial || !m->counters || !m->outbox ||
+        !m->down_out || !m->partial || !m->counters || !m->layer_counters || !m->outbox ||
         hipHostMalloc((void **)&m->outbox_host, m->outbox_floats * 4, hipHostMallocDefault) !=
             hipSuccess ||
-        hipMemset(m->counters, 0, 256 * 4) != hipSuccess) {
+        hipMemset(m->counters, 0, 256 * 4) != hipSuccess ||
+        hipMemset(m->layer_counters, 0, L * kLayerCounterWords * 4) != hipSuccess) {
         (void)hipGetLastError();
         release_model(m);
         return problem(m, "cannot allocate decode workspace");
@@ -616,7 +625,9 @@ int encode_decode(plamo_metal *m, struct model *model, const DecodePlan &plan, i
     float *stage = m->outbox + V + 2 * h;
     HIP_TRY(m, hipMemcpyAsync(m->params_dev, m->params_host, sizeof(StepParams),
                               hipMemcpyHostToDevice, s));
-    HIP_TRY(m, launch_embed(s, m->embedding, nullptr, m->params_dev, 1, (uint32_t)h, m->state_a));
+    // The embedding launch also zeroes the one-launch layers' phase counters.
+    HIP_TRY(m, launch_embed(s, m->embedding, nullptr, m->params_dev, 1, (uint32_t)h, m->state_a,
+                            m->layer_counters, (uint32_t)(L * kLayerCounterWords / kLaneStride)));
     ++n;
     float *cur = m->state_a, *nxt = m->state_b;
     const int blocks = 2 * m->cus;
@@ -636,18 +647,10 @@ int encode_decode(plamo_metal *m, struct model *model, const DecodePlan &plan, i
             p1.state_out = nxt;
         }
         uint64_t qkv_rows = (uint64_t)(d.qh + 2 * d.kh) * d.dim;
-        HIP_TRY(m, launch_gemv(s, d.qkv, qkv_rows, h, p1, m->qkv, 0, blocks));
-        ++n;
-        if (i) std::swap(cur, nxt);
         const bool shift = plan.shift[i], stale = plan.stale[i];
-        if (stale && !shift) {
-            uint32_t rows = m->params_host->count[i];
-            HIP_TRY(m, launch_rerotate(s, d.k, d.rot, rope.table, rows, d.kh, d.dim));
-            ++n;
-        }
         float *layer_stage = stage + i * 3 * m->max_width;
-        bool fused_o = false;
-        if (!shift && d.fused) {
+        // Attention over the materialized rotated rows (no sliding shift).
+        auto attention_args = [&]() {
             DecodeAttention da{};
             da.qkv = m->qkv;
             da.qn = qn;
@@ -671,6 +674,60 @@ int encode_decode(plamo_metal *m, struct model *model, const DecodePlan &plan, i
             da.kh = d.kh;
             da.dim = d.dim;
             da.splits = decode_attention_splits(d.rows);
+            return da;
+        };
+        if (!shift && d.fused && m->layer_launch) {
+            // The rotated rows are refreshed first (they do not depend on
+            // this step's projections).
+            LayerStep ls{};
+            ls.qkv_w = d.qkv;
+            ls.pq = p1;
+            ls.qkv = m->qkv;
+            ls.qkv_rows = (uint32_t)qkv_rows;
+            ls.a = attention_args();
+            ls.o_w = d.o;
+            ls.branch = m->branch;
+            ls.gu_w = d.gu;
+            ls.act = m->act;
+            ls.down_w = d.down;
+            ls.down_out = m->down_out;
+            ls.hidden = (uint32_t)h;
+            ls.inter = d.inter;
+            ls.phase = m->layer_counters + i * kLayerCounterWords;
+            ls.error = &m->params_dev->error;
+            float *in = cur, *out = nxt;
+            if (i) std::swap(in, out);
+            ls.pg.src = in;
+            ls.pg.w = mpre;
+            ls.pg.offset = 1.0f;
+            ls.pg.branch = m->branch;
+            ls.pg.rw = post;
+            ls.pg.roffset = kAttentionOffset;
+            ls.pg.state_out = out;
+            if (layer_plan(ls, (uint32_t)blocks)) {
+                if (stale) {
+                    uint32_t rows = m->params_host->count[i];
+                    HIP_TRY(m, launch_rerotate(s, d.k, d.rot, rope.table, rows, d.kh, d.dim));
+                    ++n;
+                }
+                HIP_TRY(m, launch_layer(s, ls));
+                ++n;
+                cur = out;
+                nxt = in;
+                continue;
+            }
+        }
+        HIP_TRY(m, launch_gemv(s, d.qkv, qkv_rows, h, p1, m->qkv, 0, blocks));
+        ++n;
+        if (i) std::swap(cur, nxt);
+        if (stale && !shift) {
+            uint32_t rows = m->params_host->count[i];
+            HIP_TRY(m, launch_rerotate(s, d.k, d.rot, rope.table, rows, d.kh, d.dim));
+            ++n;
+        }
+        bool fused_o = false;
+        if (!shift && d.fused) {
+            DecodeAttention da = attention_args();
             if (attention_o_supported(d.dim, d.qh / d.kh, (uint64_t)d.qh * d.dim) &&
                 !((uintptr_t)d.o & 15)) {
                 AttentionO ao{};
@@ -904,6 +961,7 @@ struct plamo_metal *plamo_metal_open(const struct plamo_metal_config *config, ch
         return nullptr;
     }
     m->cus = prop.multiProcessorCount;
+    if (const char *e = getenv("PLAMO_HIP_LAYER_LAUNCH")) m->layer_launch = atoi(e) != 0;
     snprintf(m->info.device, sizeof m->info.device, "%s (%s, %d CUs)", prop.name,
              prop.gcnArchName, prop.multiProcessorCount);
     snprintf(m->info.precision, sizeof m->info.precision, "fp32");

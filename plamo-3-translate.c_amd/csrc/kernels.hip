@@ -112,6 +112,70 @@ __device__ __forceinline__ bool arrive_last(uint32_t *counter, uint32_t expected
     return *flag;
 }
 
+// Dependencies between the phases of a chained launch (blocks ordered by
+// phase; a block waits only on lower-numbered blocks, which are dispatched
+// before it and never wait on it). A gate waits until *counter >= target; the
+// wait is bounded, and a block that gives up sets *error and writes NaN
+// results (they surface as a failed argmax). A signal counts a block in after
+// its results are written through to the coherence point.
+// A phase's arrivals are spread over `lanes` counters kLaneStride words
+// apart (block b counts on lane b % lanes): hundreds of blocks finishing
+// together would otherwise queue their atomics on one address.
+struct Gate {
+    const uint32_t *counter;
+    uint32_t lanes;
+    uint32_t target;
+    uint32_t *error;
+};
+struct Signal {
+    uint32_t *counter;
+    uint32_t lanes;
+};
+// One thread polls (a block of pollers would put thousands of requests per
+// microsecond on the counter's memory channel); the barrier then releases the
+// block. The barrier waits for LDS only, so loads issued before it stay in
+// flight.
+__device__ __forceinline__ bool gate_wait(const Gate &g) {
+    if (!g.counter) return true;
+    __shared__ int gate_open;
+    if (threadIdx.x == 0) {
+        uint32_t spins = 0;
+        int open = 1;
+        auto arrived = [&]() {
+            uint32_t sum = 0;
+            for (uint32_t l = 0; l < g.lanes; ++l)
+                sum += __hip_atomic_load(const_cast<uint32_t *>(g.counter + l * kLaneStride),
+                                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            return sum;
+        };
+        while (arrived() < g.target) {
+            __builtin_amdgcn_s_sleep(2);
+            if (++spins == (1u << 22)) {
+                atomicOr(g.error, 1u);
+                open = 0;
+                break;
+            }
+        }
+        gate_open = open;
+    }
+    __syncthreads();
+    return gate_open != 0;
+}
+__device__ __forceinline__ void signal_done(const Signal &s, uint32_t bid) {
+    if (!s.counter) return;
+    wait_stores();
+    __syncthreads();
+    if (threadIdx.x == 0)
+        __hip_atomic_fetch_add(s.counter + (bid % s.lanes) * kLaneStride, 1u, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void put(float *p, float v, bool through) {
+    if (through)
+        store_through(p, v);
+    else
+        *p = v;
+}
+
 // 1 / sqrt(mean(x^2) + 1e-6) for a 256-thread block (tests/rmsnorm_reference.s:8-21
 // arithmetic per element; the sum is a fixed tree).
 __device__ float block_rms_inverse(const float *x, uint32_t n, float *red) {
@@ -200,8 +264,13 @@ hipError_t launch_rope_table(hipStream_t stream, const float *freq, float scale,
 __global__ __launch_bounds__(kThreads) void embed_kernel(const uint16_t *embedding,
                                                          const uint32_t *ids,
                                                          const StepParams *params,
-                                                         uint32_t hidden, float *out) {
+                                                         uint32_t hidden, float *out,
+                                                         uint32_t *clear, uint32_t clear_count) {
     uint32_t t = blockIdx.y;
+    if (clear && t == 0)
+        for (uint32_t i = blockIdx.x * kThreads + threadIdx.x; i < clear_count;
+             i += gridDim.x * kThreads)
+            clear[(uint64_t)i * kLaneStride] = 0;
     uint32_t id = ids ? ids[t] : params->token;
     const uint16_t *row = embedding + (uint64_t)id * hidden;
     float *o = out + (uint64_t)t * hidden;
@@ -210,10 +279,12 @@ __global__ __launch_bounds__(kThreads) void embed_kernel(const uint16_t *embeddi
 }
 
 hipError_t launch_embed(hipStream_t stream, const uint16_t *embedding, const uint32_t *ids,
-                        const StepParams *params, uint32_t tokens, uint32_t hidden, float *out) {
+                        const StepParams *params, uint32_t tokens, uint32_t hidden, float *out,
+                        uint32_t *clear, uint32_t clear_count) {
     unsigned bx = (hidden + kThreads - 1) / kThreads;
     if (bx > 16) bx = 16;
-    embed_kernel<<<dim3(bx, tokens), kThreads, 0, stream>>>(embedding, ids, params, hidden, out);
+    embed_kernel<<<dim3(bx, tokens), kThreads, 0, stream>>>(embedding, ids, params, hidden, out,
+                                                            clear, clear_count);
     return hipGetLastError();
 }
 
@@ -266,138 +337,133 @@ __device__ __forceinline__ void gemv_accumulate(const float *xs, uint64_t chunks
 
 template <bool SWIGLU>
 __device__ __forceinline__ void gemv_store(float *y, uint64_t rows, uint64_t pair, float acc_a,
-                                           float acc_b, uint32_t lane) {
+                                           float acc_b, uint32_t lane, bool through, bool ok) {
     acc_a = wave_sum(acc_a);
     acc_b = wave_sum(acc_b);
+    if (!ok) acc_a = acc_b = __builtin_nanf("");
     if (lane == 0) {
         if (SWIGLU) {
             float d = plamo_exp(-acc_a) + 1.0f;
-            y[pair] = (acc_a / d) * acc_b;
+            put(y + pair, (acc_a / d) * acc_b, through);
         } else {
-            y[2 * pair] = acc_a;
-            if (2 * pair + 1 < rows) y[2 * pair + 1] = acc_b;
+            put(y + 2 * pair, acc_a, through);
+            if (2 * pair + 1 < rows) put(y + 2 * pair + 1, acc_b, through);
         }
     }
 }
 
-// Decode projections with a norm prologue (or a raw input the register GEMV
-// does not cover). Vector-memory loads complete in order on CDNA, so the
-// prologue's own loads are issued first, then the first three weight batches,
-// so the norm's reductions overlap the weights in flight. The weight stream
-// keeps three batches in flight: batch i+3 is requested as batch i is consumed.
-// With SWIGLU the pair is (gate row r, up row r+half) and the output is
-// silu(gate) * up (tests/activation_reference.s:99-126).
-template <bool VEC, bool SWIGLU>
-__global__ __launch_bounds__(kThreads) void gemv_kernel(const uint16_t *__restrict__ w,
-                                                        uint64_t rows, uint64_t cols,
-                                                        Prologue pro, float *__restrict__ y,
-                                                        uint64_t half) {
-    extern __shared__ float xs[];
-    __shared__ float red[4];
-    const uint32_t n = (uint32_t)cols;
-    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const uint64_t pairs = SWIGLU ? half : (rows + 1) / 2;
-    const uint64_t chunks = cols / 8, nb = (chunks + 255) / 256;
-    const uint64_t step = (uint64_t)gridDim.x * 4;
-    const uint64_t p0 = (uint64_t)blockIdx.x * 4 + wave;
-    // Batches of this wave: nb per row pair, pairs p0, p0 + step, ...
-    const uint64_t total = p0 < pairs ? ((pairs - 1 - p0) / step + 1) * nb : 0;
-    // One-round-trip prologue: contiguous 16-element slices per thread.
-    const bool fast = pro.w && n % 16 == 0 && n <= 16 * kThreads &&
-                      !(((uintptr_t)pro.src | (uintptr_t)pro.w |
-                         (pro.branch ? ((uintptr_t)pro.branch | (uintptr_t)pro.rw) : 0)) & 15);
+// Norm prologue (src/forward.s layer entry: offset-1 RMSNorm, with the
+// previous branch's residual folded in). The one-round-trip form gives each
+// thread a contiguous 16-element slice: its loads go out in one batch, then
+// two block reductions. prologue_load issues the loads, prologue_finish
+// writes the normalized vector to LDS (and block 0 the optional state/norm
+// copies, written through when another block of the launch reads them).
+struct ProloguePart {
     float sv[16], bv[16], wv[16], rv[16];
-    const uint32_t i0 = threadIdx.x * 16;
-    const bool mine = fast && i0 < n;
-    if (mine) {
+    uint32_t i0;
+    bool fast, mine;
+};
+__device__ __forceinline__ void prologue_begin(const Prologue &pro, uint32_t n, ProloguePart &pp) {
+    pp.fast = pro.w && n % 16 == 0 && n <= 16 * kThreads &&
+              !(((uintptr_t)pro.src | (uintptr_t)pro.w |
+                 (pro.branch ? ((uintptr_t)pro.branch | (uintptr_t)pro.rw) : 0)) & 15);
+    pp.i0 = threadIdx.x * 16;
+    pp.mine = pp.fast && pp.i0 < n;
+}
+__device__ __forceinline__ void prologue_load(const Prologue &pro, ProloguePart &pp) {
+    if (pp.mine) {
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-            f32x4 a = *(const f32x4 *)(pro.src + i0 + 4 * q);
-            sv[4 * q] = a.x; sv[4 * q + 1] = a.y; sv[4 * q + 2] = a.z; sv[4 * q + 3] = a.w;
+            f32x4 a = *(const f32x4 *)(pro.src + pp.i0 + 4 * q);
+            pp.sv[4 * q] = a.x; pp.sv[4 * q + 1] = a.y; pp.sv[4 * q + 2] = a.z; pp.sv[4 * q + 3] = a.w;
         }
 #pragma unroll
         for (int q = 0; q < 2; ++q) {
-            u32x4 u = *(const u32x4 *)(pro.w + i0 + 8 * q);
+            u32x4 u = *(const u32x4 *)(pro.w + pp.i0 + 8 * q);
             uint32_t uu[4] = {u.x, u.y, u.z, u.w};
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                wv[8 * q + 2 * e] = bf16f(uu[e] & 0xffffu);
-                wv[8 * q + 2 * e + 1] = __uint_as_float(uu[e] & 0xffff0000u);
+                pp.wv[8 * q + 2 * e] = bf16f(uu[e] & 0xffffu);
+                pp.wv[8 * q + 2 * e + 1] = __uint_as_float(uu[e] & 0xffff0000u);
             }
         }
         if (pro.branch) {
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
-                f32x4 a = *(const f32x4 *)(pro.branch + i0 + 4 * q);
-                bv[4 * q] = a.x; bv[4 * q + 1] = a.y; bv[4 * q + 2] = a.z; bv[4 * q + 3] = a.w;
+                f32x4 a = *(const f32x4 *)(pro.branch + pp.i0 + 4 * q);
+                pp.bv[4 * q] = a.x; pp.bv[4 * q + 1] = a.y; pp.bv[4 * q + 2] = a.z; pp.bv[4 * q + 3] = a.w;
             }
 #pragma unroll
             for (int q = 0; q < 2; ++q) {
-                u32x4 u = *(const u32x4 *)(pro.rw + i0 + 8 * q);
+                u32x4 u = *(const u32x4 *)(pro.rw + pp.i0 + 8 * q);
                 uint32_t uu[4] = {u.x, u.y, u.z, u.w};
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    rv[8 * q + 2 * e] = bf16f(uu[e] & 0xffffu);
-                    rv[8 * q + 2 * e + 1] = __uint_as_float(uu[e] & 0xffff0000u);
+                    pp.rv[8 * q + 2 * e] = bf16f(uu[e] & 0xffffu);
+                    pp.rv[8 * q + 2 * e + 1] = __uint_as_float(uu[e] & 0xffff0000u);
                 }
             }
         }
     }
-    __builtin_amdgcn_sched_barrier(0);
-    // Three batches in flight: the first three go out before the prologue.
-    u32x4 qa0[4], qb0[4], qa1[4], qb1[4], qa2[4], qb2[4];
-    auto issue = [&](uint64_t it, u32x4(&qa)[4], u32x4(&qb)[4]) {
-        gemv_load<SWIGLU>(w, rows, cols, half, pairs, p0 + (it / nb) * step,
-                          lane + (it % nb) * 256, qa, qb);
-    };
-    if (VEC) {
-        if (total > 0) issue(0, qa0, qb0);
-        if (total > 1) issue(1, qa1, qb1);
-        if (total > 2) issue(2, qa2, qb2);
-    }
-    __builtin_amdgcn_sched_barrier(0);
-
-    if (fast) {
+}
+__device__ __forceinline__ void prologue_finish(const Prologue &pro, uint32_t n, ProloguePart &pp,
+                                                float *xs, float *red, uint32_t bid,
+                                                bool through) {
+    if (pp.fast) {
         float ss = 0.0f;
         if (pro.branch) {
-            if (mine)
+            if (pp.mine)
 #pragma unroll
                 for (int k = 0; k < 16; ++k) {
-                    float t = bv[k] * bv[k];
+                    float t = pp.bv[k] * pp.bv[k];
                     ss = ss + t;
                 }
             const float ib = block_inverse_from_partial(ss, n, red);
-            if (mine)
+            if (pp.mine)
 #pragma unroll
                 for (int k = 0; k < 16; ++k) {
-                    float b = bv[k] * ib;
-                    float scale = rv[k] + pro.roffset;
-                    sv[k] = sv[k] + b * scale;
+                    float b = pp.bv[k] * ib;
+                    float scale = pp.rv[k] + pro.roffset;
+                    pp.sv[k] = pp.sv[k] + b * scale;
                 }
-            if (blockIdx.x == 0 && pro.state_out && mine)
+            if (bid == 0 && pro.state_out && pp.mine) {
+                if (through)
 #pragma unroll
-                for (int q = 0; q < 4; ++q)
-                    *(f32x4 *)(pro.state_out + i0 + 4 * q) =
-                        f32x4{sv[4 * q], sv[4 * q + 1], sv[4 * q + 2], sv[4 * q + 3]};
+                    for (int k = 0; k < 16; ++k) store_through(pro.state_out + pp.i0 + k, pp.sv[k]);
+                else
+#pragma unroll
+                    for (int q = 0; q < 4; ++q)
+                        *(f32x4 *)(pro.state_out + pp.i0 + 4 * q) =
+                            f32x4{pp.sv[4 * q], pp.sv[4 * q + 1], pp.sv[4 * q + 2], pp.sv[4 * q + 3]};
+            }
             ss = 0.0f;
         }
-        if (mine)
+        if (pp.mine)
 #pragma unroll
             for (int k = 0; k < 16; ++k) {
-                float t = sv[k] * sv[k];
+                float t = pp.sv[k] * pp.sv[k];
                 ss = ss + t;
             }
         const float is = block_inverse_from_partial(ss, n, red);
-        if (mine)
+        if (pp.mine)
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 f32x4 x;
-                x.x = (sv[4 * q] * is) * (wv[4 * q] + pro.offset);
-                x.y = (sv[4 * q + 1] * is) * (wv[4 * q + 1] + pro.offset);
-                x.z = (sv[4 * q + 2] * is) * (wv[4 * q + 2] + pro.offset);
-                x.w = (sv[4 * q + 3] * is) * (wv[4 * q + 3] + pro.offset);
-                *(f32x4 *)(xs + i0 + 4 * q) = x;
-                if (blockIdx.x == 0 && pro.norm_out) *(f32x4 *)(pro.norm_out + i0 + 4 * q) = x;
+                x.x = (pp.sv[4 * q] * is) * (pp.wv[4 * q] + pro.offset);
+                x.y = (pp.sv[4 * q + 1] * is) * (pp.wv[4 * q + 1] + pro.offset);
+                x.z = (pp.sv[4 * q + 2] * is) * (pp.wv[4 * q + 2] + pro.offset);
+                x.w = (pp.sv[4 * q + 3] * is) * (pp.wv[4 * q + 3] + pro.offset);
+                *(f32x4 *)(xs + pp.i0 + 4 * q) = x;
+                if (bid == 0 && pro.norm_out) {
+                    if (through) {
+                        store_through(pro.norm_out + pp.i0 + 4 * q, x.x);
+                        store_through(pro.norm_out + pp.i0 + 4 * q + 1, x.y);
+                        store_through(pro.norm_out + pp.i0 + 4 * q + 2, x.z);
+                        store_through(pro.norm_out + pp.i0 + 4 * q + 3, x.w);
+                    } else {
+                        *(f32x4 *)(pro.norm_out + pp.i0 + 4 * q) = x;
+                    }
+                }
             }
         __syncthreads();
     } else if (!pro.w) {
@@ -416,24 +482,75 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(const uint16_t *__restri
             xs[i] = v;
         }
         __syncthreads();
-        if (pro.branch && blockIdx.x == 0 && pro.state_out)
-            for (uint32_t i = threadIdx.x; i < n; i += kThreads) pro.state_out[i] = xs[i];
+        if (pro.branch && bid == 0 && pro.state_out)
+            for (uint32_t i = threadIdx.x; i < n; i += kThreads) put(pro.state_out + i, xs[i], through);
         float is = block_rms_inverse(xs, n, red);
         for (uint32_t i = threadIdx.x; i < n; i += kThreads) {
             float scale = bf16f(pro.w[i]) + pro.offset;
             xs[i] = (xs[i] * is) * scale;
         }
         __syncthreads();
-        if (blockIdx.x == 0 && pro.norm_out)
-            for (uint32_t i = threadIdx.x; i < n; i += kThreads) pro.norm_out[i] = xs[i];
+        if (bid == 0 && pro.norm_out)
+            for (uint32_t i = threadIdx.x; i < n; i += kThreads) put(pro.norm_out + i, xs[i], through);
     }
+}
+
+// Decode projections with a norm prologue (or a raw input the register GEMV
+// does not cover). Vector-memory loads complete in order on CDNA, so the
+// prologue's own loads are issued first, then the first three weight batches,
+// so the norm's reductions overlap the weights in flight. The weight stream
+// keeps three batches in flight: batch i+3 is requested as batch i is consumed.
+// With SWIGLU the pair is (gate row r, up row r+half) and the output is
+// silu(gate) * up (tests/activation_reference.s:99-126).
+// One block (index bid of nblocks) of the LDS-input GEMV. With a gate the
+// weight batches go out first and the prologue's inputs are read after the
+// wait; with a signal the results are written through and the block counted.
+template <bool VEC, bool SWIGLU>
+__device__ __forceinline__ void gemv_block(const uint16_t *__restrict__ w, uint64_t rows,
+                                           uint64_t cols, const Prologue &pro,
+                                           float *__restrict__ y, uint64_t half, uint32_t bid,
+                                           uint32_t nblocks, const Gate &gate,
+                                           const Signal &sig) {
+    extern __shared__ float xs[];
+    __shared__ float red[4];
+    const bool through = sig.counter != nullptr;
+    bool ok = true;
+    const uint32_t n = (uint32_t)cols;
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint64_t pairs = SWIGLU ? half : (rows + 1) / 2;
+    const uint64_t chunks = cols / 8, nb = (chunks + 255) / 256;
+    const uint64_t step = (uint64_t)nblocks * 4;
+    const uint64_t p0 = (uint64_t)bid * 4 + wave;
+    // Batches of this wave: nb per row pair, pairs p0, p0 + step, ...
+    const uint64_t total = p0 < pairs ? ((pairs - 1 - p0) / step + 1) * nb : 0;
+    ProloguePart pp;
+    prologue_begin(pro, n, pp);
+    if (!gate.counter) prologue_load(pro, pp);
+    __builtin_amdgcn_sched_barrier(0);
+    // Three batches in flight: the first three go out before the prologue.
+    u32x4 qa0[4], qb0[4], qa1[4], qb1[4], qa2[4], qb2[4];
+    auto issue = [&](uint64_t it, u32x4(&qa)[4], u32x4(&qb)[4]) {
+        gemv_load<SWIGLU>(w, rows, cols, half, pairs, p0 + (it / nb) * step,
+                          lane + (it % nb) * 256, qa, qb);
+    };
+    if (VEC) {
+        if (total > 0) issue(0, qa0, qb0);
+        if (total > 1) issue(1, qa1, qb1);
+        if (total > 2) issue(2, qa2, qb2);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    if (gate.counter) {
+        ok = gate_wait(gate);
+        prologue_load(pro, pp);
+    }
+    prologue_finish(pro, n, pp, xs, red, bid, through);
 
     if (VEC) {
         float acc_a = 0.0f, acc_b = 0.0f;
         auto consume = [&](uint64_t it, const u32x4(&qa)[4], const u32x4(&qb)[4]) {
             gemv_accumulate(xs, chunks, lane + (it % nb) * 256, qa, qb, acc_a, acc_b);
             if (it % nb == nb - 1) {
-                gemv_store<SWIGLU>(y, rows, p0 + (it / nb) * step, acc_a, acc_b, lane);
+                gemv_store<SWIGLU>(y, rows, p0 + (it / nb) * step, acc_a, acc_b, lane, through, ok);
                 acc_a = acc_b = 0.0f;
             }
         };
@@ -471,9 +588,18 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(const uint16_t *__restri
                 acc_a = __builtin_fmaf(bf16f(wa[k]), xs[k], acc_a);
                 acc_b = __builtin_fmaf(bf16f(wb[k]), xs[k], acc_b);
             }
-            gemv_store<SWIGLU>(y, rows, p, acc_a, acc_b, lane);
+            gemv_store<SWIGLU>(y, rows, p, acc_a, acc_b, lane, through, ok);
         }
     }
+    signal_done(sig, bid);
+}
+
+template <bool VEC, bool SWIGLU>
+__global__ __launch_bounds__(kThreads) void gemv_kernel(const uint16_t *__restrict__ w,
+                                                        uint64_t rows, uint64_t cols,
+                                                        Prologue pro, float *__restrict__ y,
+                                                        uint64_t half) {
+    gemv_block<VEC, SWIGLU>(w, rows, cols, pro, y, half, blockIdx.x, gridDim.x, Gate{}, Signal{});
 }
 
 // Raw-input projections (attention output, MLP down): each lane keeps its
@@ -481,17 +607,18 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(const uint16_t *__restri
 // columns, and a wave streams U rows at a time. No LDS staging of x, so the
 // 16K-column down projection is not occupancy-limited by LDS.
 template <int KC, int WPR, int U>
-__global__ __launch_bounds__(kThreads) void gemv_reg_kernel(const uint16_t *__restrict__ w,
-                                                            uint64_t rows, uint64_t cols,
-                                                            const float *__restrict__ src,
-                                                            float *__restrict__ y) {
+__device__ __forceinline__ void reg_block(const uint16_t *__restrict__ w, uint64_t rows,
+                                          uint64_t cols, const float *__restrict__ src,
+                                          float *__restrict__ y, uint32_t bid, uint32_t nblocks,
+                                          const Gate &gate, const Signal &sig) {
     constexpr int GROUPS = 4 / WPR;
     __shared__ float part[4][U];
+    const bool through = sig.counter != nullptr;
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const uint32_t pidx = wave % WPR, grp = wave / WPR;
     const uint64_t col0 = (uint64_t)pidx * KC * 512 + lane * 8;
     const uint64_t units = (rows + U - 1) / U;
-    const uint64_t step = (uint64_t)gridDim.x * GROUPS;
+    const uint64_t step = (uint64_t)nblocks * GROUPS;
     u32x4 wv[U][KC];
     auto load = [&](uint64_t unit) {
 #pragma unroll
@@ -503,8 +630,9 @@ __global__ __launch_bounds__(kThreads) void gemv_reg_kernel(const uint16_t *__re
             for (int c = 0; c < KC; ++c) wv[u][c] = __builtin_nontemporal_load(p + c * 64);
         }
     };
-    const uint64_t ubase = (uint64_t)blockIdx.x * GROUPS;
+    const uint64_t ubase = (uint64_t)bid * GROUPS;
     if (ubase + grp < units) load(ubase + grp);
+    const bool ok = gate_wait(gate);
     float x[KC][8];
 #pragma unroll
     for (int c = 0; c < KC; ++c) {
@@ -530,13 +658,13 @@ __global__ __launch_bounds__(kThreads) void gemv_reg_kernel(const uint16_t *__re
                     a = __builtin_fmaf(__uint_as_float(q[e] & 0xffff0000u), x[c][2 * e + 1], a);
                 }
             }
-            acc[u] = wave_sum(a);
+            acc[u] = ok ? wave_sum(a) : __builtin_nanf("");
         }
         if (WPR == 1) {
             if (lane == 0 && valid)
 #pragma unroll
                 for (int u = 0; u < U; ++u)
-                    if (unit * U + u < rows) y[unit * U + u] = acc[u];
+                    if (unit * U + u < rows) put(y + unit * U + u, acc[u], through);
         } else {
             if (lane == 0)
 #pragma unroll
@@ -548,11 +676,112 @@ __global__ __launch_bounds__(kThreads) void gemv_reg_kernel(const uint16_t *__re
                     float t = part[wave][u];
 #pragma unroll
                     for (int q = 1; q < WPR; ++q) t += part[wave + q][u];
-                    if (unit * U + u < rows) y[unit * U + u] = t;
+                    if (unit * U + u < rows) put(y + unit * U + u, t, through);
                 }
             __syncthreads();
         }
     }
+    signal_done(sig, bid);
+}
+
+template <int KC, int WPR, int U>
+__global__ __launch_bounds__(kThreads) void gemv_reg_kernel(const uint16_t *__restrict__ w,
+                                                            uint64_t rows, uint64_t cols,
+                                                            const float *__restrict__ src,
+                                                            float *__restrict__ y) {
+    reg_block<KC, WPR, U>(w, rows, cols, src, y, blockIdx.x, gridDim.x, Gate{}, Signal{});
+}
+
+// Decode projections with a norm prologue, x held in registers: the block
+// normalizes x into LDS, then every wave copies the whole vector into its
+// registers (lane l holds columns 512c + 8l .. 512c + 8l + 7) and streams U
+// rows per step; with SWIGLU the step is the pair (gate row p, up row
+// p + half) and the output silu(gate) * up (tests/activation_reference.s:99-126).
+// The first rows' weights are requested before the prologue's reductions.
+template <int KC, int U, bool SWIGLU>
+__device__ __forceinline__ void regp_block(const uint16_t *__restrict__ w, uint64_t rows,
+                                           uint64_t cols, const Prologue &pro,
+                                           float *__restrict__ y, uint64_t half, uint32_t bid,
+                                           uint32_t nblocks, const Gate &gate,
+                                           const Signal &sig) {
+    static_assert(!SWIGLU || U == 2, "a SwiGLU step is one gate/up row pair");
+    extern __shared__ float xs[];
+    __shared__ float red[4];
+    const bool through = sig.counter != nullptr;
+    const uint32_t n = (uint32_t)cols;
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint64_t units = SWIGLU ? half : (rows + U - 1) / U;
+    const uint64_t step = (uint64_t)nblocks * 4;
+    const uint64_t u0 = (uint64_t)bid * 4 + wave;
+    ProloguePart pp;
+    prologue_begin(pro, n, pp);
+    if (!gate.counter) prologue_load(pro, pp);
+    __builtin_amdgcn_sched_barrier(0);
+    u32x4 wv[U][KC];
+    auto load = [&](uint64_t unit) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            uint64_t r = SWIGLU ? unit + u * half : unit * U + u;
+            if (r >= rows) r = rows - 1;
+            const u32x4 *p = (const u32x4 *)(w + r * cols + lane * 8);
+#pragma unroll
+            for (int c = 0; c < KC; ++c) wv[u][c] = __builtin_nontemporal_load(p + c * 64);
+        }
+    };
+    if (u0 < units) load(u0);
+    __builtin_amdgcn_sched_barrier(0);
+    bool ok = true;
+    if (gate.counter) {
+        ok = gate_wait(gate);
+        prologue_load(pro, pp);
+    }
+    prologue_finish(pro, n, pp, xs, red, bid, through);
+    float x[KC][8];
+#pragma unroll
+    for (int c = 0; c < KC; ++c) {
+        const f32x4 a = *(const f32x4 *)(xs + c * 512 + lane * 8);
+        const f32x4 b = *(const f32x4 *)(xs + c * 512 + lane * 8 + 4);
+        x[c][0] = a.x; x[c][1] = a.y; x[c][2] = a.z; x[c][3] = a.w;
+        x[c][4] = b.x; x[c][5] = b.y; x[c][6] = b.z; x[c][7] = b.w;
+    }
+    for (uint64_t unit = u0; unit < units; unit += step) {
+        if (unit != u0) load(unit);
+        float acc[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            float a = 0.0f;
+#pragma unroll
+            for (int c = 0; c < KC; ++c) {
+                const uint32_t q[4] = {wv[u][c].x, wv[u][c].y, wv[u][c].z, wv[u][c].w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    a = __builtin_fmaf(bf16f(q[e] & 0xffffu), x[c][2 * e], a);
+                    a = __builtin_fmaf(__uint_as_float(q[e] & 0xffff0000u), x[c][2 * e + 1], a);
+                }
+            }
+            acc[u] = ok ? wave_sum(a) : __builtin_nanf("");
+        }
+        if (lane == 0) {
+            if (SWIGLU) {
+                const float d = plamo_exp(-acc[0]) + 1.0f;
+                put(y + unit, (acc[0] / d) * acc[1], through);
+            } else {
+#pragma unroll
+                for (int u = 0; u < U; ++u)
+                    if (unit * U + u < rows) put(y + unit * U + u, acc[u], through);
+            }
+        }
+    }
+    signal_done(sig, bid);
+}
+
+template <int KC, int U, bool SWIGLU>
+__global__ __launch_bounds__(kThreads) void gemv_regp_kernel(const uint16_t *__restrict__ w,
+                                                             uint64_t rows, uint64_t cols,
+                                                             Prologue pro, float *__restrict__ y,
+                                                             uint64_t half) {
+    regp_block<KC, U, SWIGLU>(w, rows, cols, pro, y, half, blockIdx.x, gridDim.x, Gate{},
+                              Signal{});
 }
 
 // Column counts the register GEMV covers: cols = 512 * KC * WPR.
@@ -611,11 +840,44 @@ static hipError_t gemv_variant(hipStream_t stream, const uint16_t *w, uint64_t r
     return hipGetLastError();
 }
 
+// Register-x prologue GEMV for widths of whole 512-column chunks. Grid: one
+// step (U rows or a gate/up pair) per wave at most; SwiGLU streams twice the
+// rows per output and takes twice the blocks.
+template <int KC>
+static hipError_t regp_variant(hipStream_t stream, const uint16_t *w, uint64_t rows,
+                               uint64_t cols, const Prologue &pro, float *y, uint64_t half,
+                               int blocks_hint) {
+    const uint64_t units = half ? half : (rows + 1) / 2;
+    uint64_t blocks = (units + 3) / 4;
+    const uint64_t cap = blocks_hint > 0 ? (uint64_t)blocks_hint * (half ? 2 : 1) : blocks;
+    if (blocks > cap) blocks = cap;
+    const size_t lds = cols * sizeof(float);
+    if (half)
+        gemv_regp_kernel<KC, 2, true><<<(unsigned)blocks, kThreads, lds, stream>>>(w, rows, cols, pro, y, half);
+    else
+        gemv_regp_kernel<KC, 2, false><<<(unsigned)blocks, kThreads, lds, stream>>>(w, rows, cols, pro, y, 0);
+    return hipGetLastError();
+}
+
+static bool regp_launch(hipStream_t stream, const uint16_t *w, uint64_t rows, uint64_t cols,
+                        const Prologue &pro, float *y, uint64_t half, int blocks_hint,
+                        hipError_t *status) {
+    if (!pro.w || cols % 512 || ((uintptr_t)w & 15)) return false;
+    switch (cols / 512) {
+    case 4: *status = regp_variant<4>(stream, w, rows, cols, pro, y, half, blocks_hint); return true;
+    case 5: *status = regp_variant<5>(stream, w, rows, cols, pro, y, half, blocks_hint); return true;
+    case 8: *status = regp_variant<8>(stream, w, rows, cols, pro, y, half, blocks_hint); return true;
+    case 12: *status = regp_variant<12>(stream, w, rows, cols, pro, y, half, blocks_hint); return true;
+    default: return false;
+    }
+}
+
 hipError_t launch_gemv(hipStream_t stream, const uint16_t *w, uint64_t rows, uint64_t cols,
                        const Prologue &pro, float *y, uint64_t swiglu_half, int blocks_hint) {
     hipError_t status;
     if (!pro.w && !swiglu_half && gemv_reg_launch(stream, w, rows, cols, pro.src, y, blocks_hint, &status))
         return status;
+    if (regp_launch(stream, w, rows, cols, pro, y, swiglu_half, blocks_hint, &status)) return status;
     bool vec = cols % 8 == 0 && ((uintptr_t)w & 15) == 0;
     if (swiglu_half)
         return vec ? gemv_variant<true, true>(stream, w, rows, cols, pro, y, swiglu_half, blocks_hint)
@@ -1214,17 +1476,17 @@ constexpr uint32_t kAttnWaves = 8, kAttnThreads = 64 * kAttnWaves;
 // One pass of 8 rows per wave: a block loads at most 64 K and V rows, so a
 // context is spread over many CUs (one CU's load path is the limit otherwise).
 constexpr uint32_t kRowsPerBlock = 64;
-template <int G>
-constexpr uint32_t attention_rows_per_wave() { return 8; }
 
 // One attention block (KV head kvh, row split `split`). With `done`, the block
 // that completes a KV head's output writes it through to the coherence point
 // and counts the head in *done (the fused O projection waits on it).
-template <int DIM, int G>
+template <int DIM, int G, int W>
 __device__ __forceinline__ void attention_block(const DecodeAttention &a, uint32_t kvh,
-                                                uint32_t split, uint32_t *done) {
-    constexpr uint32_t RW = attention_rows_per_wave<G>();
-    constexpr uint32_t P = kAttnWaves * RW;  // rows per pass
+                                                uint32_t split, uint32_t *done,
+                                                const Gate &gate) {
+    constexpr uint32_t RW = kRowsPerBlock / W;  // rows per wave
+    constexpr uint32_t P = W * RW;              // rows per pass (one block)
+    constexpr int HPW = (G + W - 1) / W;        // query heads per wave
     constexpr int PL = DIM / 64;             // value columns per lane
     constexpr int KD = DIM / 16;             // key dims per lane
     constexpr int KR = RW / 4;               // key rows per lane
@@ -1239,23 +1501,40 @@ __device__ __forceinline__ void attention_block(const DecodeAttention &a, uint32
     float *knew = qs + G * DIM;                  // [DIM] rotated new key
     float *vnew = knew + DIM;                    // [DIM]
     float *sc = vnew + DIM;                      // [kRowsPerBlock + 1][G]
-    float *wpart = sc + (kRowsPerBlock + 1) * G; // [kAttnWaves][G][DIM]
+    float *wpart = sc + (kRowsPerBlock + 1) * G; // [W][G][DIM]
 
-    // Count-independent operands: wave g < G normalizes query head g, the last
-    // wave the new key; lane j < DIM/2 holds elements j and j + DIM/2.
-    // Loaded unconditionally (lanes and waves with no use read valid data they
-    // ignore) and kept as raw bits until used, so no wait is forced here.
-    const bool qwave = wave < (uint32_t)G, kwave = wave == kAttnWaves - 1;
+    // The step's query/key/value heads: wave w normalizes query heads w,
+    // w + W, ..., the last wave the new key; lane j < DIM/2 holds elements j
+    // and j + DIM/2. Loaded unconditionally (lanes and waves with no use read
+    // valid data they ignore) and kept as raw bits until used. Without a gate
+    // they go out first (they do not depend on the row count); with a gate
+    // (they are produced by an earlier phase of the launch) after the cached
+    // K/V rows, which do not depend on them.
+    const bool kwave = wave == W - 1;
     const bool hl = lane < HALF;
     const uint32_t hj = lane % HALF;
-    const float *qsrc = a.qkv + (uint64_t)(kvh * G + (qwave ? wave : 0)) * DIM;
-    const float *ksrc = a.qkv + (uint64_t)(a.qh + kvh) * DIM;
-    const float *vsrc = a.qkv + (uint64_t)(a.qh + a.kh + kvh) * DIM;
-    const float qx[2] = {qsrc[hj], qsrc[hj + HALF]};
-    const uint32_t qwb[2] = {a.qn[hj], a.qn[hj + HALF]};
-    const float kx[2] = {ksrc[hj], ksrc[hj + HALF]};
-    const uint32_t kwb[2] = {a.kn[hj], a.kn[hj + HALF]};
-    const float vx[2] = {vsrc[hj], vsrc[hj + HALF]};
+    float qx[HPW][2], kx[2], vx[2];
+    uint32_t qwb[2], kwb[2];
+    auto load_inputs = [&]() {
+#pragma unroll
+        for (int h = 0; h < HPW; ++h) {
+            const uint32_t g = wave + h * W;
+            const float *qsrc = a.qkv + (uint64_t)(kvh * G + (g < (uint32_t)G ? g : 0)) * DIM;
+            qx[h][0] = qsrc[hj];
+            qx[h][1] = qsrc[hj + HALF];
+        }
+        const float *ksrc = a.qkv + (uint64_t)(a.qh + kvh) * DIM;
+        const float *vsrc = a.qkv + (uint64_t)(a.qh + a.kh + kvh) * DIM;
+        qwb[0] = a.qn[hj];
+        qwb[1] = a.qn[hj + HALF];
+        kx[0] = ksrc[hj];
+        kx[1] = ksrc[hj + HALF];
+        kwb[0] = a.kn[hj];
+        kwb[1] = a.kn[hj + HALF];
+        vx[0] = vsrc[hj];
+        vx[1] = vsrc[hj + HALF];
+    };
+    if (!gate.counter) load_inputs();
 
     const uint32_t count = a.params->count[a.layer];
     const uint32_t n = count + 1;
@@ -1271,7 +1550,11 @@ __device__ __forceinline__ void attention_block(const DecodeAttention &a, uint32
     // is scored from LDS.
     const uint32_t hr = hi < count ? hi : count;
     const float *cs = a.table + (uint64_t)count * DIM;
-    const float rc = cs[hj], rs = cs[HALF + hj];
+    float rc = 0.0f, rs = 0.0f;
+    if (!gate.counter) {
+        rc = cs[hj];
+        rs = cs[HALF + hj];
+    }
 
     // Every lane loads unconditionally, also past the range (branches around
     // loads make the compiler wait for every load in flight where paths
@@ -1330,22 +1613,32 @@ __device__ __forceinline__ void attention_block(const DecodeAttention &a, uint32
     __builtin_amdgcn_sched_barrier(0);
     load_v(base0, vc0);
     __builtin_amdgcn_sched_barrier(0);
+    bool ok = true;
+    if (gate.counter) {
+        ok = gate_wait(gate);
+        load_inputs();
+        rc = cs[hj];
+        rs = cs[HALF + hj];
+    }
 
     // Offset-1 head RMSNorm then split-half rotation (src/qkv.s:36-67,
     // tests/rope_reference.s:14-30).
-    if (qwave) {
-        float ss = hl ? qx[0] * qx[0] : 0.0f;
-        float t = hl ? qx[1] * qx[1] : 0.0f;
+#pragma unroll
+    for (int h = 0; h < HPW; ++h) {
+        const uint32_t g = wave + h * W;
+        if (g >= (uint32_t)G) break;
+        float ss = hl ? qx[h][0] * qx[h][0] : 0.0f;
+        float t = hl ? qx[h][1] * qx[h][1] : 0.0f;
         ss = wave_sum(ss + t);
         float ms = ss / (float)DIM;
         ms = ms + 0.000001f;
         const float inv = 1.0f / __builtin_sqrtf(ms);
         if (hl) {
-            float va = (qx[0] * inv) * (bf16f(qwb[0]) + 1.0f);
-            float vb = (qx[1] * inv) * (bf16f(qwb[1]) + 1.0f);
+            float va = (qx[h][0] * inv) * (bf16f(qwb[0]) + 1.0f);
+            float vb = (qx[h][1] * inv) * (bf16f(qwb[1]) + 1.0f);
             float p0 = va * rc, p1 = vb * rs, p2 = vb * rc, p3 = va * rs;
-            qs[wave * DIM + lane] = p0 - p1;
-            qs[wave * DIM + lane + HALF] = p2 + p3;
+            qs[g * DIM + lane] = p0 - p1;
+            qs[g * DIM + lane + HALF] = p2 + p3;
         }
     }
     if (kwave && owner) {
@@ -1440,8 +1733,7 @@ __device__ __forceinline__ void attention_block(const DecodeAttention &a, uint32
 
     // Phase 2: per head, the maximum over the block's rows, exp in place, sum.
     const uint32_t rows = (owner ? count + 1 : hr) - lo;
-    if (qwave) {
-        const uint32_t g = wave;
+    for (uint32_t g = wave; g < (uint32_t)G; g += W) {
         float mx = -__builtin_inff();
         for (uint32_t r = lane; r < rows; r += 64) mx = fmaxf(mx, sc[r * G + g]);
         mx = wave_max(mx);
@@ -1511,13 +1803,13 @@ __device__ __forceinline__ void attention_block(const DecodeAttention &a, uint32
 #pragma unroll
         for (int e = 0; e < PL; ++e) wpart[(wave * G + g) * DIM + lane * PL + e] = acc[g][e];
     __syncthreads();
-    for (uint32_t i = threadIdx.x; i < G * DIM; i += kAttnThreads) {
+    for (uint32_t i = threadIdx.x; i < G * DIM; i += W * 64) {
         const uint32_t g = i / DIM, d = i % DIM;
         float o = 0.0f;
 #pragma unroll
-        for (uint32_t w = 0; w < kAttnWaves; ++w) o = o + wpart[(w * G + g) * DIM + d];
+        for (uint32_t w = 0; w < (uint32_t)W; ++w) o = o + wpart[(w * G + g) * DIM + d];
         if (splits == 1) {
-            const float r = o / stats[g][1];
+            const float r = ok ? o / stats[g][1] : __builtin_nanf("");
             if (done)
                 store_through(a.out + (uint64_t)(kvh * G + g) * DIM + d, r);
             else
@@ -1525,7 +1817,7 @@ __device__ __forceinline__ void attention_block(const DecodeAttention &a, uint32
         } else {
             float *bp = a.partial + ((uint64_t)(kvh * a.splits + split) * G + g) * rec;
             if (d == 0) {
-                store_through(bp, stats[g][0]);
+                store_through(bp, ok ? stats[g][0] : __builtin_nanf(""));
                 store_through(bp + 1, stats[g][1]);
             }
             store_through(bp + 2 + d, o);
@@ -1537,7 +1829,7 @@ __device__ __forceinline__ void attention_block(const DecodeAttention &a, uint32
     }
     // The last block of this KV head merges the partials.
     if (!arrive_last(&a.counters[kvh], splits, &is_last)) return;
-    for (uint32_t i = threadIdx.x; i < G * DIM; i += kAttnThreads) {
+    for (uint32_t i = threadIdx.x; i < G * DIM; i += W * 64) {
         const uint32_t g = i / DIM, d = i % DIM;
         const float *bp = a.partial + ((uint64_t)kvh * a.splits * G + g) * rec;
         float mx = -__builtin_inff();
@@ -1560,7 +1852,7 @@ __device__ __forceinline__ void attention_block(const DecodeAttention &a, uint32
 
 template <int DIM, int G>
 __global__ __launch_bounds__(kAttnThreads) void decode_attention_kernel(DecodeAttention a) {
-    attention_block<DIM, G>(a, blockIdx.x, blockIdx.y, nullptr);
+    attention_block<DIM, G, kAttnWaves>(a, blockIdx.x, blockIdx.y, nullptr, Gate{});
 }
 
 // Attention fused with the output projection (src/mixer.s:60-80: O = W_o .
@@ -1623,7 +1915,8 @@ template <int DIM, int G, int KC>
 __global__ __launch_bounds__(kAttnThreads) void attention_o_kernel(AttentionO f) {
     const uint32_t attention_blocks = f.a.kh * f.a.splits;
     if (blockIdx.x < attention_blocks)
-        attention_block<DIM, G>(f.a, blockIdx.x % f.a.kh, blockIdx.x / f.a.kh, f.done);
+        attention_block<DIM, G, kAttnWaves>(f.a, blockIdx.x % f.a.kh, blockIdx.x / f.a.kh, f.done,
+                                            Gate{});
     else
         oproj_block<KC>(f, blockIdx.x - attention_blocks);
 }
@@ -1637,8 +1930,8 @@ uint32_t decode_attention_splits(uint64_t rows) {
     return (uint32_t)((rows + kRowsPerBlock - 1) / kRowsPerBlock);
 }
 
-static size_t decode_attention_lds(uint32_t dim, uint32_t group) {
-    return (group * dim + 2 * dim + (kRowsPerBlock + 1) * group + kAttnWaves * group * dim) *
+static size_t decode_attention_lds(uint32_t dim, uint32_t group, uint32_t waves = kAttnWaves) {
+    return (group * dim + 2 * dim + (kRowsPerBlock + 1) * group + waves * group * dim) *
            sizeof(float);
 }
 
@@ -1716,6 +2009,126 @@ hipError_t launch_decode_attention(hipStream_t stream, const DecodeAttention &a)
     if (!decode_attention_supported(a.dim, a.qh / a.kh) || a.splits < 1 || a.splits > 65535)
         return hipErrorInvalidValue;
     return a.dim == 64 ? decode_attention_dim<64>(stream, a) : decode_attention_dim<128>(stream, a);
+}
+
+// ---------------------------------------------------------------- fused layer
+// One decoder layer of a decode step (src/forward.s layer loop: src/mixer.s
+// QKV, attention and O; src/mlp.s gate/up, SwiGLU and down) as one launch.
+// Blocks are ordered by phase: [QKV | attention | O | gate/up | down]. A
+// block of a later phase first requests its weights, then waits until every
+// block of the phase it reads has counted itself, so one phase's tail
+// overlaps the next phase's weight stream instead of a launch boundary
+// draining the GPU between them. Every wait is on lower-numbered blocks,
+// which are dispatched first, so it ends; it is also bounded (a block that
+// gives up writes NaN and sets the error flag).
+// Coherence: whatever a phase reads from an earlier phase of the launch (the
+// QKV output, the attention output, the O output, the residual state, the
+// SwiGLU output) is read by no block before its wait, so no cache holds a
+// stale copy; producers write it through to the coherence point and wait
+// for the stores before counting themselves.
+constexpr int kLayerAttnWaves = (int)(kThreads / 64);
+
+template <int DIM, int G, int OKC, int OWPR, int OU, int DKC, int DWPR, int DU>
+__global__ __launch_bounds__(kThreads) void layer_kernel(LayerStep l) {
+    uint32_t b = blockIdx.x;
+    const uint32_t na = l.a.kh * l.a.splits;
+    if (b < l.nq) {
+        gemv_block<true, false>(l.qkv_w, l.qkv_rows, l.hidden, l.pq, l.qkv, 0, b, l.nq, Gate{},
+                                Signal{l.phase, kPhaseLanes});
+        return;
+    }
+    b -= l.nq;
+    if (b < na) {
+        attention_block<DIM, G, kLayerAttnWaves>(l.a, b % l.a.kh, b / l.a.kh, l.phase + kPhaseWords,
+                                                 Gate{l.phase, kPhaseLanes, l.nq, l.error});
+        return;
+    }
+    b -= na;
+    if (b < l.no) {
+        reg_block<OKC, OWPR, OU>(l.o_w, l.hidden, (uint64_t)l.a.qh * DIM, l.a.out, l.branch, b,
+                                 l.no, Gate{l.phase + kPhaseWords, 1, l.a.kh, l.error},
+                                 Signal{l.phase + 2 * kPhaseWords, kPhaseLanes});
+        return;
+    }
+    b -= l.no;
+    if (b < l.ng) {
+        gemv_block<true, true>(l.gu_w, 2ull * l.inter, l.hidden, l.pg, l.act, l.inter, b, l.ng,
+                               Gate{l.phase + 2 * kPhaseWords, kPhaseLanes, l.no, l.error},
+                               Signal{l.phase + 3 * kPhaseWords, kPhaseLanes});
+        return;
+    }
+    b -= l.ng;
+    if (b < l.nd)
+        reg_block<DKC, DWPR, DU>(l.down_w, l.hidden, l.inter, l.act, l.down_out, b, l.nd,
+                                 Gate{l.phase + 3 * kPhaseWords, kPhaseLanes, l.ng, l.error},
+                                 Signal{});
+}
+
+// Shapes with a fused variant: the register GEMV configuration of the O and
+// down projections is the one the separate launches use for those widths.
+enum LayerVariant { kLayerNone, kLayerG4O2048D8192, kLayerG4O2048D10240, kLayerG4O4096D16384,
+                    kLayerG6O6144D24576 };
+
+static LayerVariant layer_variant(const LayerStep &l) {
+    if (l.a.dim != 128 || !l.a.kh || l.a.qh % l.a.kh) return kLayerNone;
+    const uint32_t g = l.a.qh / l.a.kh, ocols = l.a.qh * l.a.dim;
+    if (g == 4 && ocols == 2048 && l.inter == 8192) return kLayerG4O2048D8192;
+    if (g == 4 && ocols == 2048 && l.inter == 10240) return kLayerG4O2048D10240;
+    if (g == 4 && ocols == 4096 && l.inter == 16384) return kLayerG4O4096D16384;
+    if (g == 6 && ocols == 6144 && l.inter == 24576) return kLayerG6O6144D24576;
+    return kLayerNone;
+}
+
+template <int DIM, int G, int OKC, int OWPR, int OU, int DKC, int DWPR, int DU>
+static void layer_counts(LayerStep &l, uint32_t hint) {
+    auto cap = [&](uint64_t n) { return (uint32_t)(n < hint ? (n ? n : 1) : hint); };
+    l.nq = cap((((uint64_t)l.qkv_rows + 1) / 2 + 3) / 4);
+    l.no = cap((((uint64_t)l.hidden + OU - 1) / OU + (4 / OWPR) - 1) / (4 / OWPR));
+    l.ng = cap(((uint64_t)l.inter + 3) / 4);
+    l.nd = cap((((uint64_t)l.hidden + DU - 1) / DU + (4 / DWPR) - 1) / (4 / DWPR));
+}
+
+template <int DIM, int G, int OKC, int OWPR, int OU, int DKC, int DWPR, int DU>
+static hipError_t layer_launch(hipStream_t stream, const LayerStep &l) {
+    const void *k = (const void *)layer_kernel<DIM, G, OKC, OWPR, OU, DKC, DWPR, DU>;
+    size_t lds = std::max<size_t>((size_t)l.hidden * sizeof(float),
+                                  decode_attention_lds(DIM, G, kLayerAttnWaves));
+    if (lds > 65536) {
+        hipError_t e = hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) return e;
+    }
+    const uint64_t grid = (uint64_t)l.nq + (uint64_t)l.a.kh * l.a.splits + l.no + l.ng + l.nd;
+    layer_kernel<DIM, G, OKC, OWPR, OU, DKC, DWPR, DU>
+        <<<(unsigned)grid, kThreads, lds, stream>>>(l);
+    return hipGetLastError();
+}
+
+bool layer_plan(LayerStep &l, uint32_t blocks_hint) {
+    // The fused variant's GEMVs are the vector forms: 16-byte aligned weight
+    // rows and inputs, widths in whole 512-column chunks where registers hold x.
+    const uintptr_t align = (uintptr_t)l.qkv_w | (uintptr_t)l.o_w | (uintptr_t)l.gu_w |
+                            (uintptr_t)l.down_w | (uintptr_t)l.a.out | (uintptr_t)l.act;
+    if ((align & 15) || l.hidden % 8 || !blocks_hint || !l.phase || !l.error) return false;
+    if (!l.a.splits || l.a.splits > 65535) return false;
+    if (l.qkv_rows != (l.a.qh + 2 * l.a.kh) * l.a.dim) return false;
+    switch (layer_variant(l)) {
+    case kLayerG4O2048D8192: layer_counts<128, 4, 4, 1, 2, 8, 2, 1>(l, blocks_hint); return true;
+    case kLayerG4O2048D10240: layer_counts<128, 4, 4, 1, 2, 5, 4, 1>(l, blocks_hint); return true;
+    case kLayerG4O4096D16384: layer_counts<128, 4, 8, 1, 2, 8, 4, 1>(l, blocks_hint); return true;
+    case kLayerG6O6144D24576: layer_counts<128, 6, 6, 2, 2, 12, 4, 1>(l, blocks_hint); return true;
+    default: return false;
+    }
+}
+
+hipError_t launch_layer(hipStream_t stream, const LayerStep &l) {
+    if (!l.nq || !l.no || !l.ng || !l.nd || !l.phase || !l.error) return hipErrorInvalidValue;
+    switch (layer_variant(l)) {
+    case kLayerG4O2048D8192: return layer_launch<128, 4, 4, 1, 2, 8, 2, 1>(stream, l);
+    case kLayerG4O2048D10240: return layer_launch<128, 4, 4, 1, 2, 5, 4, 1>(stream, l);
+    case kLayerG4O4096D16384: return layer_launch<128, 4, 8, 1, 2, 8, 4, 1>(stream, l);
+    case kLayerG6O6144D24576: return layer_launch<128, 6, 6, 2, 2, 12, 4, 1>(stream, l);
+    default: return hipErrorInvalidValue;
+    }
 }
 
 // ---------------------------------------------------------------- prompt attention

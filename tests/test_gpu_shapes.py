@@ -60,14 +60,35 @@ def test_c1_single_layer_prefilled_kv():
         syn.close()
 
 
-def test_c4_shapes_four_layers():
+@pytest.mark.parametrize("layer_launch", ["1", "0"])
+def test_c4_shapes_four_layers(monkeypatch, layer_launch):
     # Pinned host arrays: the decode graph writes logits, state, normalized
     # state and the new K/V rows into them in place (the bench's setup).
+    # layer_launch 1: each decoder layer is one launch with phase-chained
+    # blocks; 0: one launch per projection and the attention.
+    monkeypatch.setenv("PLAMO_HIP_LAYER_LAUNCH", layer_launch)
+    say(f"c4 four layers, layer launch {layer_launch}")
     cfg = dict(plamo_hip.CONFIGS["c4"], layers=4, vocab=1000)
     syn = plamo_hip.Synthetic(**cfg, pattern=4, seed=202)
     try:
         run_pair(syn, steps=4, prompt=list(range(5, 5 + 69 * 7, 7)), pinned=True)
         run_pair(syn, steps=2, prompt=list(range(3, 3 + 20 * 5, 5)))
+    finally:
+        syn.close()
+
+
+@pytest.mark.parametrize("name", ["c3", "c5"])
+def test_layer_launch_variants(monkeypatch, name):
+    # The remaining one-launch layer shapes: C3 (hidden 2560, down 10240
+    # columns) and C5 (hidden 6144, six query heads per KV head, O 6144 and
+    # down 24576 columns), two layers each, with prefilled KV rows so the
+    # attention spans several blocks per KV head.
+    monkeypatch.setenv("PLAMO_HIP_LAYER_LAUNCH", "1")
+    cfg = dict(plamo_hip.CONFIGS[name], layers=2, vocab=500)
+    say(f"{name} two layers")
+    syn = plamo_hip.Synthetic(**cfg, embedding_std=1.0, seed=505)
+    try:
+        run_pair(syn, steps=3, prompt=None, fill=300, pinned=True)
     finally:
         syn.close()
 
