@@ -268,7 +268,7 @@ def main() -> int:
                                   "frac_of_split_bf16": round(ttft_flop / ttft[128] / 1e9 /
                                                               SPLIT_BF16_CEILING_TFLOPS, 4)}
                                  if 128 in ttft else None),
-        "roofline": {"bound": "hbm", "kernel": "gemv_kernel<VEC,SWIGLU> (gate/up + SwiGLU)",
+        "roofline": {"bound": "hbm", "kernel": "gemv_regp_kernel<8,2,SWIGLU> (gate/up + SwiGLU)",
                      "achieved": dom["GBps"], "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(dom["GBps"] / HBM_PEAK_GBPS, 4), "traffic": traffic},
         "kernels": kernels,

@@ -1,8 +1,8 @@
 """GPU parity at the BASELINE.json shapes (the production fast paths).
 
 C1: one layer, hidden 2048, 16/4 heads of 128, MLP 8192, KV
-pre-filled with 512 rows of raw K/V ~ N(0,1) (rotations rebuilt by the first
-step on both sides); then decode steps and a prompt.
+pre-filled with 512 (then 254) rows of raw K/V ~ N(0,1) (rotations rebuilt by
+the first step on both sides); then decode steps and a prompt.
 C4 shapes with 4 of its 32 layers and a small vocabulary:
 covers the 16K-column down projection and the fused attention at group 4.
 C2 in full: 16 layers, vocab 100000, a 32-token prompt and 64
@@ -55,6 +55,9 @@ def test_c1_single_layer_prefilled_kv():
     syn = plamo_hip.Synthetic(**cfg, embedding_std=1.0, seed=101)
     try:
         run_pair(syn, steps=6, prompt=None, fill=512)
+        # 255 -> 257 rows: four splits per KV head merged by the O projection,
+        # then five merged by the last attention block.
+        run_pair(syn, steps=3, prompt=None, fill=254)
         run_pair(syn, steps=3, prompt=[3, 9, 1, 15, 0, 7, 2, 11, 4, 5, 13, 6, 8], fill=0)
     finally:
         syn.close()
