@@ -1687,7 +1687,11 @@ __device__ __forceinline__ void attention_block(const DecodeAttention &a, uint32
 
     // Phase 1: scores of the cached rows, then of the appended row.
     const float scale = 1.0f / __builtin_sqrtf((float)DIM);
+    // All G x KR dot products and their reductions are formed before any is
+    // stored: the chains are independent, and a masked store between them
+    // would split the code into blocks the scheduler cannot interleave.
     auto score = [&](uint32_t base, const float (&kc)[KR][KD]) {
+        float s[G][KR];
 #pragma unroll
         for (int g = 0; g < G; ++g) {
             float q[KD];
@@ -1701,12 +1705,23 @@ __device__ __forceinline__ void attention_block(const DecodeAttention &a, uint32
             }
 #pragma unroll
             for (int j = 0; j < KR; ++j) {
-                float s = 0.0f;
+                float t = 0.0f;
 #pragma unroll
-                for (int i = 0; i < KD; ++i) s = __builtin_fmaf(q[i], kc[j][i], s);
-                s = row_sum16(s);
+                for (int i = 0; i < KD; ++i) t = __builtin_fmaf(q[i], kc[j][i], t);
+                s[g][j] = t;
+            }
+        }
+#pragma unroll
+        for (int g = 0; g < G; ++g)
+#pragma unroll
+            for (int j = 0; j < KR; ++j) s[g][j] = row_sum16(s[g][j]);
+        if ((lane & 15) == 0) {
+#pragma unroll
+            for (int j = 0; j < KR; ++j) {
                 const uint32_t row = base + rg + 4 * j;
-                if ((lane & 15) == 0 && row < hr) sc[(row - lo) * G + g] = s * scale;
+                if (row < hr)
+#pragma unroll
+                    for (int g = 0; g < G; ++g) sc[(row - lo) * G + g] = s[g][j] * scale;
             }
         }
     };
@@ -1827,20 +1842,44 @@ __device__ __forceinline__ void attention_block(const DecodeAttention &a, uint32
         if (done) arrive_last(done, 0xffffffffu, &is_last);
         return;
     }
-    // The last block of this KV head merges the partials.
+    // The last block of this KV head merges the partials. They were written
+    // through by the other blocks before they counted themselves, and no
+    // block of this launch has read them before, so plain loads see them (the
+    // launch started with invalidated caches); up to kMergeBatch splits are
+    // loaded in one round trip.
     if (!arrive_last(&a.counters[kvh], splits, &is_last)) return;
+    constexpr uint32_t kMergeBatch = 8;
     for (uint32_t i = threadIdx.x; i < G * DIM; i += W * 64) {
         const uint32_t g = i / DIM, d = i % DIM;
         const float *bp = a.partial + ((uint64_t)kvh * a.splits * G + g) * rec;
-        float mx = -__builtin_inff();
-        for (uint32_t sI = 0; sI < splits; ++sI)
-            mx = fmaxf(mx, load_through(bp + (uint64_t)sI * G * rec));
-        float sum = 0.0f, o = 0.0f;
-        for (uint32_t sI = 0; sI < splits; ++sI) {
-            const float *q = bp + (uint64_t)sI * G * rec;
-            const float f = plamo_exp(load_through(q) - mx);
-            sum = __builtin_fmaf(load_through(q + 1), f, sum);
-            o = __builtin_fmaf(load_through(q + 2 + d), f, o);
+        float mx = -__builtin_inff(), sum = 0.0f, o = 0.0f;
+        if (splits <= kMergeBatch) {
+            float m[kMergeBatch], l[kMergeBatch], v[kMergeBatch];
+#pragma unroll
+            for (uint32_t sI = 0; sI < kMergeBatch; ++sI) {
+                const float *q = bp + (uint64_t)(sI < splits ? sI : 0) * G * rec;
+                m[sI] = q[0];
+                l[sI] = q[1];
+                v[sI] = q[2 + d];
+            }
+#pragma unroll
+            for (uint32_t sI = 0; sI < kMergeBatch; ++sI)
+                if (sI < splits) mx = fmaxf(mx, m[sI]);
+#pragma unroll
+            for (uint32_t sI = 0; sI < kMergeBatch; ++sI) {
+                if (sI >= splits) break;
+                const float f = plamo_exp(m[sI] - mx);
+                sum = __builtin_fmaf(l[sI], f, sum);
+                o = __builtin_fmaf(v[sI], f, o);
+            }
+        } else {
+            for (uint32_t sI = 0; sI < splits; ++sI) mx = fmaxf(mx, bp[(uint64_t)sI * G * rec]);
+            for (uint32_t sI = 0; sI < splits; ++sI) {
+                const float *q = bp + (uint64_t)sI * G * rec;
+                const float f = plamo_exp(q[0] - mx);
+                sum = __builtin_fmaf(q[1], f, sum);
+                o = __builtin_fmaf(q[2 + d], f, o);
+            }
         }
         if (done)
             store_through(a.out + (uint64_t)(kvh * G + g) * DIM + d, o / sum);
@@ -1864,9 +1903,18 @@ __global__ __launch_bounds__(kAttnThreads) void decode_attention_kernel(DecodeAt
 // its dot products: the O weights cross HBM while attention runs. The wait is
 // bounded; a block that gives up writes NaN rows (they surface as a failed
 // argmax) and sets *error.
+// O rows per wave of the fused kernel, and the LDS every block of it claims:
+// more than half of a CU's 160 KiB, so a CU holds one block. With the KV
+// rows allocated in small steps the launch (64 attention blocks at C4 below
+// 512 rows plus 171 O blocks) then fits the 256 CUs at once: every O block
+// requests its weights at the start, and no O block's 128 KB of weight loads
+// shares a CU's load path with an attention block's latency-bound loads.
+constexpr int kORows = 3;
+constexpr size_t kAttentionOLds = 96 * 1024;
+
 template <int KC>
 __device__ __forceinline__ void oproj_block(const AttentionO &f, uint32_t ob) {
-    constexpr int U = 2;  // rows per wave
+    constexpr int U = kORows;
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const uint32_t r0 = (ob * kAttnWaves + wave) * U;
     if (r0 >= f.rows) return;
@@ -1887,7 +1935,9 @@ __device__ __forceinline__ void oproj_block(const AttentionO &f, uint32_t ob) {
             break;
         }
     }
-    float acc[U] = {0.0f, 0.0f};
+    float acc[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) acc[u] = 0.0f;
 #pragma unroll
     for (int c = 0; c < KC; ++c) {
         const f32x4 *xp = (const f32x4 *)(f.x + c * 512 + lane * 8);
@@ -1960,13 +2010,11 @@ static hipError_t decode_attention_dim(hipStream_t stream, const DecodeAttention
 
 template <int DIM, int G, int KC>
 static hipError_t attention_o_variant(hipStream_t stream, const AttentionO &f) {
-    size_t lds = decode_attention_lds(DIM, G);
-    if (lds > 65536) {
-        hipError_t e = hipFuncSetAttribute((const void *)attention_o_kernel<DIM, G, KC>,
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-        if (e != hipSuccess) return e;
-    }
-    const uint32_t oblocks = (f.rows + 2 * kAttnWaves - 1) / (2 * kAttnWaves);
+    const size_t lds = std::max(decode_attention_lds(DIM, G), kAttentionOLds);
+    hipError_t e = hipFuncSetAttribute((const void *)attention_o_kernel<DIM, G, KC>,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return e;
+    const uint32_t oblocks = (f.rows + kORows * kAttnWaves - 1) / (kORows * kAttnWaves);
     attention_o_kernel<DIM, G, KC>
         <<<f.a.kh * f.a.splits + oblocks, kAttnThreads, lds, stream>>>(f);
     return hipGetLastError();
