@@ -14,6 +14,7 @@ import ctypes
 import numpy as np
 import pytest
 
+import prompt_cache
 from parity import compare, gate, oracle_lib, plamo_hip, say, tiny
 
 pytestmark = pytest.mark.gpu
@@ -231,6 +232,59 @@ def test_host_edits_are_uploaded():
                     inst.rotation(i).scale_bits = 0
             assert be.forward(a, 9) == 1 and oracle_lib.forward(b, 9)
             compare(a, b)
+        clean(be)
+    finally:
+        be.close()
+        a.close()
+        b.close()
+        s.close()
+
+
+@pytest.mark.parametrize("pinned", [False, True])
+def test_prompt_prefix_cache_flows(pinned):
+    # The engine's request pattern (runtime/engine.c:337-381 prepare,
+    # 451-481 translate): two template prefixes prefilled on the GPU and
+    # captured at startup; each request resets the model, restores its
+    # direction's prefix (runtime/prompt_cache.c, restated in
+    # tests/prompt_cache.py), prefills the suffix and decodes greedily.
+    # Requests alternate directions, include a miss (ids that do not start
+    # with the prefix: full prefill) and a direction without a prefix. Every
+    # request is checked against the oracle running the whole prompt from a
+    # reset model. (A sliding window larger than the prefixes: the reference
+    # captures only when every layer holds exactly the prefix rows.)
+    s = tiny(h=128, inter=257, dim=128, capacity=300, window=48)
+    a, b = s.instance(pinned=pinned), s.instance()
+    be = plamo_hip.Backend(s)
+    try:
+        prefixes = [[1, 4, 9, 16, 3, 8, 2, 11, 5, 7, 10, 6], [2, 13, 5, 8, 1, 14, 9, 3, 12]]
+        snaps = []
+        for ids in prefixes:
+            a.reset()
+            assert be.prefill(a, ids) == 1
+            snaps.append(prompt_cache.capture(a, ids))
+            assert snaps[-1] is not None
+        a.reset()
+        requests = [(1, 9), (2, 14), (1, 23), (0, 11), (2, 6), (1, -1)]
+        for n, (direction, extra) in enumerate(requests):
+            if extra < 0:  # a miss: same length as a hit, wrong first id
+                ids = [15] + prefixes[0][1:] + [4, 4, 7]
+            else:
+                base = prefixes[direction - 1] if direction else []
+                ids = base + [(n * 7 + j * 3) % 17 for j in range(extra)]
+            say(f"prefix request {n}: direction {direction}, {len(ids)} ids")
+            a.reset()
+            b.reset()
+            cached = prompt_cache.restore(snaps[direction - 1], a, ids) if direction else 0
+            expect = len(prefixes[direction - 1]) if direction and extra >= 0 else 0
+            assert cached == expect
+            assert be.prefill(a, ids[cached:]) == 1
+            assert oracle_lib.prefill(b, ids)
+            compare(a, b)
+            for step in range(4):
+                token = prompt_cache.greedy(b)
+                assert be.forward(a, token) == 1
+                assert oracle_lib.forward(b, token)
+                compare(a, b)
         clean(be)
     finally:
         be.close()
