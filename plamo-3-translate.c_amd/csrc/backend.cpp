@@ -10,6 +10,7 @@
 #include "../../include/plamo_backend.h"
 #include "../../include/plamo_compute.h"
 #include "../../include/plamo_diag.h"
+#include "../../include/plamo_draft.h"
 #include "kernels.h"
 
 #include <hip/hip_runtime.h>
@@ -1538,6 +1539,43 @@ int plamo_metal_commit(struct plamo_metal *m, struct model *model, uint64_t inde
     remember(m, model);
     ++m->verification_index;
     ++m->info.committed_tokens;
+    return 1;
+}
+
+// Lowers every layer's count by `steps` on host and device. The rows below the
+// new count are untouched by the undone steps unless a sliding window was full
+// (its rows shifted each step), so nothing is uploaded: the shadow is moved
+// with the host counts and the next step appends at the lower count. Rotated
+// rows stay valid when they were (positions are row indices).
+int plamo_hip_rewind(struct plamo_metal *m, struct model *model, uint64_t steps) {
+    if (!m || !model) return 0;
+    if (!steps) return 1;
+    if (m->model != model || m->layers.size() != model->count) return 0;
+    for (uint64_t i = 0; i < model->count; ++i) {
+        const Layer &d = m->layers[i];
+        const struct mixer *mx = model->layers[i]->mixer;
+        const struct cache *c = mx->cache;
+        if (!d.synced || d.count != c->count || d.processed != mx->rotation->processed_count ||
+            d.scale_bits != mx->rotation->scale_bits || c->count < steps ||
+            (c->sliding && c->count >= c->capacity))
+            return 0;
+    }
+    m->verification_tokens = 0;
+    for (uint64_t i = 0; i < model->count; ++i) {
+        struct mixer *mx = model->layers[i]->mixer;
+        struct cache *c = mx->cache;
+        struct rotation *r = mx->rotation;
+        bool rotated = r->processed_count == c->count;
+        c->count -= steps;
+        if (rotated) {
+            r->processed_count = c->count;
+        } else {
+            r->processed_count = 0;
+            r->scale_bits = 0;
+        }
+        mx->gqa->tokens = c->count;
+    }
+    remember(m, model);
     return 1;
 }
 

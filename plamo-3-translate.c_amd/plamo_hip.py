@@ -133,6 +133,26 @@ class CpuPath(Structure):
                                               f32p))]
 
 
+class DraftStats(Structure):
+    """struct plamo_hip_draft_stats (include/plamo_draft.h)."""
+    _fields_ = [(name, c_uint64) for name in (
+        "proposals", "proposed_tokens", "accepted_tokens", "draft_steps", "device_rewinds",
+        "host_restores")] + [("horizon", c_uint)]
+
+
+class DecodeResult(Structure):
+    """struct plamo_hip_decode_result (include/plamo_draft.h)."""
+    _fields_ = [(name, c_uint64) for name in (
+        "completion_tokens", "decode_steps", "speculative_batches", "speculative_tokens",
+        "proposed_tokens", "accepted_tokens")] + [
+        ("draft_seconds", c_double), ("decode_seconds", c_double), ("finish", c_uint)]
+
+
+TOKEN_FN = ctypes.CFUNCTYPE(c_int, c_uint32, c_void_p)
+TOKENIZE_FN = ctypes.CFUNCTYPE(c_uint64, c_void_p, c_char_p, c_uint, POINTER(POINTER(c_uint32)))
+DRAFT_MAX = 16  # runtime/draft.h:5
+
+
 # Symbols each public header declares (checked by the ABI tests).
 EXPORTS = {
     "plamo_model.h": ["plamo_prefill", "plamo_forward", "plamo_argmax"],
@@ -146,6 +166,13 @@ EXPORTS = {
                         "plamo_metal_prefill", "plamo_metal_verify", "plamo_metal_commit",
                         "plamo_metal_linear", "plamo_metal_mlp"],
     "plamo_diag.h": ["plamo_hip_time_kernel"],
+    "plamo_draft.h": ["plamo_draft_open", "plamo_draft_close", "plamo_draft_reset",
+                      "plamo_draft_propose", "plamo_draft_accept", "plamo_draft_checkpoint",
+                      "plamo_draft_restore", "plamo_draft_checkpoint_free",
+                      "plamo_hip_draft_open", "plamo_hip_draft_install",
+                      "plamo_hip_draft_set_tokenizer", "plamo_hip_draft_reset_ids",
+                      "plamo_hip_draft_get_stats", "plamo_hip_draft_next_horizon",
+                      "plamo_hip_decode", "plamo_hip_rewind"],
     "plamo_synthetic.h": ["plamo_synthetic_defaults", "plamo_synthetic_build",
                           "plamo_synthetic_free", "plamo_synthetic_weights",
                           "plamo_synthetic_frequencies", "plamo_synthetic_instantiate",
@@ -189,6 +216,24 @@ def load() -> ctypes.CDLL:
         "plamo_register_cpu_path": (None, [POINTER(CpuPath)]),
         "plamo_hip_time_kernel": (c_int, [c_void_p, M, c_uint64, c_int, c_int,
                                           POINTER(c_double), POINTER(c_double)]),
+        "plamo_draft_open": (c_void_p, []),
+        "plamo_draft_close": (None, [c_void_p]),
+        "plamo_draft_reset": (c_int, [c_void_p, c_char_p, c_uint]),
+        "plamo_draft_propose": (c_uint, [c_void_p, c_uint32, c_uint, POINTER(c_uint32)]),
+        "plamo_draft_accept": (c_int, [c_void_p, c_uint]),
+        "plamo_draft_checkpoint": (c_void_p, [M, c_uint]),
+        "plamo_draft_restore": (c_int, [c_void_p, c_uint, c_uint]),
+        "plamo_draft_checkpoint_free": (None, [c_void_p]),
+        "plamo_hip_draft_open": (c_void_p, [M, POINTER(MetalConfig), c_char_p, c_size_t]),
+        "plamo_hip_draft_install": (None, [c_void_p]),
+        "plamo_hip_draft_set_tokenizer": (None, [c_void_p, TOKENIZE_FN, c_void_p]),
+        "plamo_hip_draft_reset_ids": (c_int, [c_void_p, POINTER(c_uint32), c_uint64]),
+        "plamo_hip_draft_get_stats": (None, [c_void_p, POINTER(DraftStats)]),
+        "plamo_hip_draft_next_horizon": (c_uint, [c_uint, c_uint, c_uint, c_uint]),
+        "plamo_hip_decode": (c_int, [c_void_p, M, POINTER(c_void_p), POINTER(c_uint32), c_uint64,
+                                     c_uint, c_uint, TOKEN_FN, c_void_p, POINTER(DecodeResult),
+                                     c_char_p, c_size_t]),
+        "plamo_hip_rewind": (c_int, [c_void_p, M, c_uint64]),
         "plamo_synthetic_defaults": (None, [POINTER(SyntheticConfig)] + [c_uint64] * 7),
         "plamo_synthetic_build": (c_void_p, [POINTER(SyntheticConfig), c_uint, c_char_p,
                                              c_size_t]),
@@ -416,3 +461,76 @@ class Backend:
         if self.handle:
             self.lib.plamo_metal_close(self.handle)
             self.handle = None
+
+
+class Draft:
+    """In-process proposer (include/plamo_draft.h) over a synthetic draft model
+    instance; the draft backend is its own plamo_metal handle."""
+
+    def __init__(self, synthetic: Synthetic, inst: Instance):
+        lib = load()
+        self.lib = lib
+        self.synthetic = synthetic
+        self.inst = inst
+        self._maps = (Mapping * 1)(synthetic.mapping)
+        cfg = MetalConfig()
+        cfg.maps = self._maps
+        cfg.count = 1
+        err = ctypes.create_string_buffer(1024)
+        self.handle = c_void_p(lib.plamo_hip_draft_open(inst.model_ptr, ctypes.byref(cfg), err,
+                                                        1024))
+        if not self.handle.value:
+            raise RuntimeError(err.value.decode())
+
+    def reset_ids(self, ids) -> int:
+        arr = (c_uint32 * len(ids))(*ids)
+        return self.lib.plamo_hip_draft_reset_ids(self.handle, arr, len(ids))
+
+    def propose(self, first: int, limit: int):
+        out = (c_uint32 * DRAFT_MAX)()
+        n = self.lib.plamo_draft_propose(self.handle, first, limit, out)
+        return list(out)[:n]
+
+    def accept(self, consumed: int) -> int:
+        return self.lib.plamo_draft_accept(self.handle, consumed)
+
+    def stats(self) -> DraftStats:
+        out = DraftStats()
+        self.lib.plamo_hip_draft_get_stats(self.handle, ctypes.byref(out))
+        return out
+
+    def release(self):
+        """Hands the handle to a caller that takes ownership (plamo_hip_decode)."""
+        h, self.handle = self.handle, c_void_p(None)
+        return h
+
+    def close(self):
+        if self.handle.value:
+            self.lib.plamo_draft_close(self.handle)
+            self.handle = c_void_p(None)
+
+
+def decode(backend: Backend, inst: Instance, prompt, max_tokens: int, draft: Draft | None = None,
+           block: int = 0, cancel_after: int | None = None):
+    """plamo_hip_decode over a prefilled instance: (tokens, DecodeResult, draft
+    still open). The draft, if any, is closed by the library when it fails."""
+    lib = load()
+    tokens = []
+
+    def on_token(token_id, _ctx):
+        tokens.append(int(token_id))
+        return 0 if cancel_after is not None and len(tokens) >= cancel_after else 1
+
+    cb = TOKEN_FN(on_token)
+    handle = c_void_p(draft.handle.value if draft is not None else None)
+    arr = (c_uint32 * max(1, len(prompt)))(*prompt)
+    result = DecodeResult()
+    err = ctypes.create_string_buffer(256)
+    ok = lib.plamo_hip_decode(backend.handle, inst.model_ptr, ctypes.byref(handle), arr,
+                              len(prompt), max_tokens, block, cb, None, ctypes.byref(result),
+                              err, 256)
+    if draft is not None and not handle.value:
+        draft.handle = c_void_p(None)  # closed by the library
+    if not ok:
+        raise RuntimeError(err.value.decode())
+    return tokens, result, handle.value is not None
