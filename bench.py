@@ -141,6 +141,115 @@ def measured_traffic():
     return None
 
 
+def speculative(args) -> dict:
+    """the 31B-class model (C5, tied embedding/head) with
+    the 0.8B-class model (C2 shape) as the in-process draft, 4 draft tokens
+    per verify (a 5-token batched verify), a 455-token prompt and 128 greedy
+    tokens through the engine's decode loop (runtime/engine.c:514-566,
+    plamo_hip_decode). Speculation must leave the tokens unchanged; with
+    unrelated random weights the draft is rarely right, so the acceptance
+    measured here is a property of the synthetic weights, and the per-round
+    component times are reported beside it."""
+    tcfg = dict(plamo_hip.CONFIGS["c5"])
+    tied = tcfg.pop("tied", 0)
+    dcfg = dict(plamo_hip.CONFIGS["c2"])
+    threads = min(16, os.cpu_count() or 1)
+    t0 = time.perf_counter()
+    target = plamo_hip.Synthetic(**tcfg, tied=tied, seed=20261201, threads=threads)
+    source = plamo_hip.Synthetic(**dcfg, seed=20261202, threads=threads)
+    log(f"synthetic c5 ({target.mapping.bytes / 1e9:.1f} GB) and c2 draft "
+        f"({source.mapping.bytes / 1e9:.1f} GB) in {time.perf_counter() - t0:.1f} s")
+    inst, d_inst = target.instance(pinned=True), source.instance(pinned=True)
+    be = plamo_hip.Backend(target)
+    draft = plamo_hip.Draft(source, d_inst)
+    block, max_tokens = 5, 128
+    rng = np.random.default_rng(11)
+    prompt = rng.integers(0, tcfg["vocab"], size=455).astype(np.uint32).tolist()
+
+    def run(with_draft, n):
+        inst.reset()
+        if be.prefill(inst, prompt) != 1:
+            raise RuntimeError(be.info().note.decode())
+        return plamo_hip.decode(be, inst, prompt, n, draft=draft if with_draft else None,
+                                block=block)
+
+    run(False, 4)  # graph capture and workspace growth
+    run(True, 8)
+    plain, r0, _ = run(False, max_tokens)
+    before = draft.stats()
+    spec, r, alive = run(True, max_tokens)
+    if not alive:
+        raise RuntimeError("the draft failed during the run")
+    after = draft.stats()
+    plain_tps = r0.completion_tokens / r0.decode_seconds
+    spec_tps = r.completion_tokens / r.decode_seconds
+    log(f"plain {plain_tps:.2f} tok/s ({r0.decode_seconds / r0.decode_steps * 1e3:.3f} ms/step); "
+        f"speculative {spec_tps:.2f} tok/s, {r.accepted_tokens}/{r.proposed_tokens} accepted in "
+        f"{r.speculative_batches} verifies")
+
+    # Component times: a 5-token verify of the target, a draft step, a commit.
+    inst.reset()
+    assert be.prefill(inst, prompt) == 1
+    verify_ms = []
+    for _ in range(6):
+        start = time.perf_counter()
+        ok, _ = be.verify(inst, plain[:block])
+        verify_ms.append((time.perf_counter() - start) * 1e3)
+        assert ok == 1
+    start = time.perf_counter()
+    assert be.commit(inst, 0) == 1
+    commit_ms = (time.perf_counter() - start) * 1e3
+    assert draft.reset_ids(prompt) == 1
+    draft_ms = []
+    for _ in range(6):
+        start = time.perf_counter()
+        ids = draft.propose(plain[0], block)
+        draft_ms.append((time.perf_counter() - start) * 1e3 / max(1, len(ids) - 1))
+        assert ids and draft.accept(1)
+    step_ms = r0.decode_seconds / r0.decode_steps
+    t_verify, t_draft = float(np.median(verify_ms[1:])), float(np.median(draft_ms[1:]))
+    log(f"verify({block}) {t_verify:.3f} ms, draft step {t_draft:.3f} ms, commit {commit_ms:.3f} ms")
+    projected = {}
+    for alpha in (0.5, 0.7, 0.9):
+        tokens = sum(alpha ** i for i in range(block))  # 1 + expected accepted drafts
+        cost = (block - 1) * t_draft + t_verify + tokens * commit_ms
+        projected[str(alpha)] = round(tokens / cost * 1e3, 2)
+    info = be.info()
+    assert info.errors == 0 and info.cpu_fallbacks == 0, info.note.decode()
+    result = {
+        "metric": "speculative decode tok/s + acceptance (31B-class target, 0.8B-class draft)",
+        "value": round(spec_tps, 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "higher_is_better": True,
+        "dtype": "fp32",
+        "data": "synthetic (seeded BF16 weights ~N(0,0.02); target and draft unrelated; "
+                "uniform random prompt ids)",
+        "config": {"workload": "c5 target (tied head) + c2-shape draft in process; 455-token "
+                               "prompt, 128 greedy tokens, 4 draft tokens per verify",
+                   "block": block, "max_tokens": max_tokens},
+        "tokens_identical_to_plain": spec == plain,
+        "completion_tokens": r.completion_tokens,
+        "acceptance": round(r.accepted_tokens / max(1, r.proposed_tokens), 4),
+        "verifies": r.speculative_batches,
+        "draft_device_rewinds": after.device_rewinds - before.device_rewinds,
+        "draft_host_restores": after.host_restores - before.host_restores,
+        "draft_seconds": round(r.draft_seconds, 4),
+        "plain_tok_s": round(plain_tps, 2),
+        "components_ms": {"target_decode_step": round(step_ms * 1e3, 3),
+                          "verify_5": round(t_verify, 3), "draft_step": round(t_draft, 3),
+                          "commit": round(commit_ms, 3)},
+        "projected_tok_s_at_acceptance": projected,
+    }
+    draft.close()
+    be.close()
+    for x in (inst, d_inst):
+        x.close()
+    target.close()
+    source.close()
+    return result
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -156,12 +265,17 @@ def main() -> int:
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="also run device-to-device copies of MIB MiB (the known-size "
                          "kernel that scales rocprofv3 FETCH_SIZE / WRITE_SIZE)")
+    ap.add_argument("--speculative", action="store_true",
+                    help="measure BASELINE configs[4] (C5 target, 0.8B-class draft) instead")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path "
               f"(--gpus {args.gpus} is not supported; shard design is in DESIGN.md)",
               file=sys.stderr)
         return 2
+    if args.speculative:
+        print(json.dumps(speculative(args)), flush=True)
+        return 0
     cfg = dict(plamo_hip.CONFIGS[args.config])
     cfg["name"] = args.config
     tied = cfg.pop("tied", 0)

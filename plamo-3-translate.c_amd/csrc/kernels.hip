@@ -1278,6 +1278,212 @@ static hipError_t gemm_split_variant(hipStream_t stream, GemmSplit g, const Gemm
     return hipGetLastError();
 }
 
+// ---------------------------------------------------------------- skinny split-BF16 GEMM
+// C[t, r] = sum_k X[t, k] * W[r, k] for at most 16 tokens (candidate
+// verification, short prompts, granular projections). Weight-streaming: each
+// weight byte is read once, as in the decode GEMV. v_mfma_f32_16x16x32_bf16
+// takes 16 weight rows as M and the tokens (padded to 16 with zeros) as N;
+// each FP32 x is split into its three exact BF16 terms in registers (the split
+// of split_planes_kernel), so the products are exact and accumulate in FP32.
+//
+// Grid (row blocks, K slices). A block stages X[:, slice] in LDS once (rows
+// padded by 16 bytes against bank conflicts), then each of its 4 waves streams
+// R tiles of 16 weight rows over the slice, two steps of 32 U columns in
+// flight (register double buffer). With several K slices, each block writes
+// its tiles to the workspace and the last block of a row block adds them in
+// slice order (deterministic).
+//
+// MFMA u of a step takes columns 32 u .. 32 u + 31 and lane quarter q the 8
+// starting at 32 u + 8 q, so one load instruction reads 64 contiguous bytes of
+// each of its 16 rows. Lane layout of v_mfma_f32_16x16x32: A row and B column
+// = lane % 16; D value e of lane l is row 4 (l / 16) + e, column l % 16.
+struct SkinnyGemm {
+    const float *x;
+    uint64_t ldx;
+    const uint16_t *w;
+    uint32_t n, k, t, kc, slices;
+    float *y;
+    uint64_t ldy;
+    float *partial;
+    uint32_t *counters;
+};
+
+constexpr uint32_t kSkinnyTokens = 16;
+constexpr uint32_t kSkinnyU = 4;
+constexpr uint32_t kSkinnyStep = 32 * kSkinnyU;       // columns per step
+constexpr uint32_t kSkinnyLdsFloats = 12288;          // X slice budget per block (48 KiB)
+
+template <int R, int U>
+__global__ __launch_bounds__(256) void skinny_gemm_kernel(SkinnyGemm g) {
+    constexpr uint32_t KS = 32 * U;
+    extern __shared__ float xs[];  // [t][kc + 4]
+    __shared__ int is_last;
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t col = lane & 15, q = lane >> 4;
+    const uint32_t k0 = blockIdx.y * g.kc, stride = g.kc + 4;
+    const uint32_t r0 = (blockIdx.x * 4 + wave) * 16 * R;
+    // Stage the slice of X.
+    const uint32_t g4 = g.kc / 4;
+    for (uint32_t e = threadIdx.x; e < g.t * g4; e += 256) {
+        const uint32_t tok = e / g4, c = (e - tok * g4) * 4;
+        *(f32x4 *)(xs + tok * stride + c) =
+            *(const f32x4 *)(g.x + (uint64_t)tok * g.ldx + k0 + c);
+    }
+    const uint16_t *wr[R];
+#pragma unroll
+    for (int rt = 0; rt < R; ++rt)
+        wr[rt] = g.w + (uint64_t)min(r0 + 16 * rt + col, g.n - 1) * g.k + k0 + 8 * q;
+    const bool live = col < g.t;  // B column = token
+    const float *xl = xs + (live ? col : 0) * stride + 8 * q;
+    const uint32_t steps = g.kc / KS;  // even
+
+    f32x4 acc[R];
+#pragma unroll
+    for (int rt = 0; rt < R; ++rt) acc[rt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    u32x4 a0[R][U], a1[R][U];
+    auto load = [&](u32x4 (&a)[R][U], uint32_t s) {
+#pragma unroll
+        for (int rt = 0; rt < R; ++rt)
+#pragma unroll
+            for (int u = 0; u < U; ++u)
+                a[rt][u] = __builtin_nontemporal_load(
+                    (const u32x4 *)(wr[rt] + (uint64_t)s * KS + 32 * u));
+    };
+    auto compute = [&](const u32x4 (&a)[R][U], uint32_t s) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            f32x4 x0 = *(const f32x4 *)(xl + s * KS + 32 * u);
+            f32x4 x1 = *(const f32x4 *)(xl + s * KS + 32 * u + 4);
+            const float v8[8] = {live ? x0.x : 0.0f, live ? x0.y : 0.0f, live ? x0.z : 0.0f,
+                                 live ? x0.w : 0.0f, live ? x1.x : 0.0f, live ? x1.y : 0.0f,
+                                 live ? x1.z : 0.0f, live ? x1.w : 0.0f};
+            uint32_t h[8], md[8], lo[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                h[e] = __float_as_uint(v8[e]) & 0xffff0000u;
+                const float r = v8[e] - __uint_as_float(h[e]);
+                md[e] = __float_as_uint(r) & 0xffff0000u;
+                lo[e] = __float_as_uint(r - __uint_as_float(md[e]));
+            }
+            const bf16x8 bh = __builtin_bit_cast(
+                bf16x8, u32x4{pack_hi16(h[0], h[1]), pack_hi16(h[2], h[3]),
+                              pack_hi16(h[4], h[5]), pack_hi16(h[6], h[7])});
+            const bf16x8 bm = __builtin_bit_cast(
+                bf16x8, u32x4{pack_hi16(md[0], md[1]), pack_hi16(md[2], md[3]),
+                              pack_hi16(md[4], md[5]), pack_hi16(md[6], md[7])});
+            const bf16x8 bl = __builtin_bit_cast(
+                bf16x8, u32x4{pack_hi16(lo[0], lo[1]), pack_hi16(lo[2], lo[3]),
+                              pack_hi16(lo[4], lo[5]), pack_hi16(lo[6], lo[7])});
+#pragma unroll
+            for (int rt = 0; rt < R; ++rt) {
+                const bf16x8 av = __builtin_bit_cast(bf16x8, a[rt][u]);
+                acc[rt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bh, acc[rt], 0, 0, 0);
+                acc[rt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bm, acc[rt], 0, 0, 0);
+                acc[rt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bl, acc[rt], 0, 0, 0);
+            }
+        }
+    };
+    // Loads are unconditional inside the loop (two steps per trip, the last
+    // pair peeled) so the compiler keeps exact wait counts.
+    // sched_barrier keeps each group of loads whole and in place, so waiting
+    // for one buffer never waits for the other's prefetch.
+    load(a0, 0);
+    __syncthreads();
+    uint32_t s = 0;
+    for (; s + 2 < steps; s += 2) {
+        load(a1, s + 1);
+        __builtin_amdgcn_sched_barrier(0);
+        compute(a0, s);
+        __builtin_amdgcn_sched_barrier(0);
+        load(a0, s + 2);
+        __builtin_amdgcn_sched_barrier(0);
+        compute(a1, s + 1);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    load(a1, s + 1);
+    __builtin_amdgcn_sched_barrier(0);
+    compute(a0, s);
+    __builtin_amdgcn_sched_barrier(0);
+    compute(a1, s + 1);
+
+    if (g.slices > 1) {
+        // Tile layout [slice][row block][wave][rt][lane][4] (coalesced).
+        float *part = g.partial +
+                      (((uint64_t)blockIdx.y * gridDim.x + blockIdx.x) * 4 + wave) * R * 256;
+#pragma unroll
+        for (int rt = 0; rt < R; ++rt)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) store_through(part + (rt * 4 + e) * 64 + lane, acc[rt][e]);
+        if (!arrive_last(&g.counters[blockIdx.x], g.slices, &is_last)) return;
+        const uint64_t slice_floats = (uint64_t)gridDim.x * 4 * R * 256;
+        const float *base = g.partial + ((uint64_t)blockIdx.x * 4 + wave) * R * 256 + lane;
+#pragma unroll
+        for (int rt = 0; rt < R; ++rt)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc[rt][e] = load_through(base + (rt * 4 + e) * 64);
+        for (uint32_t sl = 1; sl < g.slices; ++sl)
+#pragma unroll
+            for (int rt = 0; rt < R; ++rt)
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    acc[rt][e] = acc[rt][e] +
+                                 load_through(base + sl * slice_floats + (rt * 4 + e) * 64);
+    }
+    if (!live) return;
+    float *yr = g.y + (uint64_t)col * g.ldy;
+#pragma unroll
+    for (int rt = 0; rt < R; ++rt) {
+        const uint32_t row = r0 + 16 * rt + 4 * q;
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            if (row + e < g.n) yr[row + e] = acc[rt][e];
+    }
+}
+
+// Slices of K: the fewest whose X slice fits the LDS budget, doubled while
+// the grid is under two blocks per CU and each slice keeps at least four
+// steps. 0 when K does not split into even step counts.
+static uint32_t skinny_slices(uint64_t cols, uint64_t tokens, uint32_t row_blocks) {
+    const uint64_t unit = 2 * kSkinnyStep;
+    if (cols % unit) return 0;
+    const uint64_t units = cols / unit;
+    uint32_t slices = 0;
+    for (uint32_t sl = 1; sl <= units && sl <= 64; ++sl)
+        if (units % sl == 0 && tokens * (cols / sl + 4) <= kSkinnyLdsFloats) {
+            slices = sl;
+            break;
+        }
+    if (!slices) return 0;
+    while ((uint64_t)row_blocks * slices < 512 && units % (2 * slices) == 0 &&
+           cols / (2 * slices) >= 2 * unit && slices < 64)
+        slices *= 2;
+    return slices;
+}
+
+template <int R>
+static hipError_t skinny_gemm_variant(hipStream_t stream, SkinnyGemm g, const GemmWorkspace *ws) {
+    const uint32_t row_blocks = (g.n + 64 * R - 1) / (64 * R);
+    uint32_t slices = skinny_slices(g.k, g.t, row_blocks);
+    if (!slices) return hipErrorInvalidValue;
+    if (slices > 1 && (!ws || !ws->partial || row_blocks > ws->counters ||
+                       (uint64_t)slices * row_blocks * 4 * R * 256 > ws->partial_floats))
+        return hipErrorInvalidValue;
+    g.slices = slices;
+    g.kc = g.k / slices;
+    g.partial = ws ? ws->partial : nullptr;
+    g.counters = ws ? ws->counter_base : nullptr;
+    const size_t lds = (size_t)g.t * (g.kc + 4) * 4;
+    skinny_gemm_kernel<R, kSkinnyU><<<dim3(row_blocks, slices), 256, lds, stream>>>(g);
+    return hipGetLastError();
+}
+
+static bool skinny_supported(const float *x, uint64_t x_stride, const uint16_t *w, uint64_t rows,
+                             uint64_t cols, uint64_t tokens) {
+    return tokens <= kSkinnyTokens && rows < (1u << 31) && cols <= (1u << 30) &&
+           x_stride % 4 == 0 && !((uintptr_t)x & 15) && !((uintptr_t)w & 15) &&
+           skinny_slices(cols, tokens, 1 << 20) != 0;
+}
+
 static bool gemm_split_supported(const float *x, uint64_t x_stride, const uint16_t *w,
                                  uint64_t cols) {
     return cols % (2 * kSplitBK) == 0 && x_stride % 4 == 0 && !((uintptr_t)x & 15) &&
@@ -1292,6 +1498,20 @@ hipError_t launch_gemm(hipStream_t stream, const float *x, uint64_t x_stride, co
                        uint64_t rows, uint64_t cols, uint64_t tokens, float *y,
                        uint64_t y_stride, const GemmWorkspace *ws) {
     if (!tokens || !rows) return hipSuccess;
+    if (skinny_supported(x, x_stride, w, rows, cols, tokens)) {
+        SkinnyGemm g{};
+        g.x = x;
+        g.ldx = x_stride;
+        g.w = w;
+        g.n = (uint32_t)rows;
+        g.k = (uint32_t)cols;
+        g.t = (uint32_t)tokens;
+        g.y = y;
+        g.ldy = y_stride;
+        hipError_t e = rows >= 16384 ? skinny_gemm_variant<2>(stream, g, ws)
+                                     : skinny_gemm_variant<1>(stream, g, ws);
+        if (e != hipErrorInvalidValue) return e;
+    }
     if (ws && ws->planes && tokens > 1 && rows < (1u << 31) && tokens < (1u << 31) &&
         gemm_split_supported(x, x_stride, w, cols) &&
         gemm_plane_elems(tokens, cols) <= ws->plane_elems) {

@@ -1,7 +1,9 @@
 """GPU parity of the prompt GEMM through plamo_metal_linear
 (runtime/metal.m:239-385): the split-BF16 matrix-core path (one and two
 32-row tiles per wave, several M tiles, N not a multiple of the tile, split-K
-with the last-block reduction) against the oracle's matmul (src/matmul.s,
+with the last-block reduction) and, for at most 16 tokens, the weight-streaming
+skinny path (one and two 16-row tiles per block, ragged last tiles, every
+token count up to 16) against the oracle's matmul (src/matmul.s,
 bit-identical to per-token matvec), with the reference's GPU gate.
 
 The three-term split of each FP32 input is exact, so the products carry no
@@ -32,7 +34,7 @@ def weights_f64(ptr, rows, cols):
     return (w.astype(np.uint32) << 16).view(np.float32).astype(np.float64).reshape(rows, cols)
 
 
-@pytest.mark.parametrize("tokens", [2, 31, 33, 64, 65, 130])
+@pytest.mark.parametrize("tokens", [1, 2, 5, 16, 17, 31, 33, 64, 65, 130])
 def test_split_bf16_gemm(oracle, tokens):
     # hidden 256, MLP 4096, vocab 300: down is N=256 x K=4096 (split-K),
     # gate/up N=8192 x K=256, head N=300 (ragged last tile) x K=256.
@@ -50,6 +52,36 @@ def test_split_bf16_gemm(oracle, tokens):
             x = rng.standard_normal((tokens, cols)).astype(np.float32)
             x[0, :8] *= 1e3   # wide dynamic range within a row
             x[-1, 8:16] *= 1e-3
+            r, y = be.linear(ptr, x, rows)
+            assert r == 1
+            gate(y, reference(oracle, ptr, x, rows), f"{name} tokens={tokens}")
+            exact = x.astype(np.float64) @ weights_f64(ptr, rows, cols).T
+            err = np.sqrt(np.sum((y - exact) ** 2) / np.sum(exact ** 2))
+            assert err <= 3e-6, f"{name}: relative L2 {err:.3g} against the float64 product"
+        info = be.info()
+        assert info.errors == 0 and info.cpu_fallbacks == 0
+    finally:
+        be.close()
+        a.close()
+        s.close()
+
+
+@pytest.mark.parametrize("tokens", [1, 3, 5, 8, 13, 16])
+def test_skinny_gemm_two_row_tiles(oracle, tokens):
+    # gate/up of MLP 8200 is N=16400 (two 16-row tiles per block, the last
+    # block half full) x K=384; down is N=384 x K=8200 is not a multiple of
+    # 128 columns and takes the tiled path.
+    s = plamo_hip.Synthetic(384, 1, 3, 1, 128, 8200, 40, window=4, global_capacity=64,
+                            pattern=1, seed=5)
+    a = s.instance()
+    be = plamo_hip.Backend(s)
+    try:
+        mlp = a.layer(0).mlp.contents
+        rng = np.random.default_rng(100 + tokens)
+        for name, ptr, rows, cols in [("gate_up", mlp.gu, 16400, 384),
+                                      ("down", mlp.down, 384, 8200)]:
+            say(f"skinny {name} tokens={tokens}")
+            x = rng.standard_normal((tokens, cols)).astype(np.float32)
             r, y = be.linear(ptr, x, rows)
             assert r == 1
             gate(y, reference(oracle, ptr, x, rows), f"{name} tokens={tokens}")
