@@ -123,12 +123,13 @@ struct plamo_metal {
     // Prompt / candidate workspace (grown on demand).
     uint64_t prompt_rows = 0;
     Buffer p_state, p_norm, p_qkv, p_q, p_attn, p_branch, p_gu, p_act, p_side_k, p_side_v,
-        p_ids, p_window, p_logits;
+        p_ids, p_window, p_logits, p_attn_split;
     uint32_t *ids_host = nullptr;
     // Candidate results kept for commit.
     float *v_state = nullptr, *v_norm = nullptr, *v_logits = nullptr, *v_prop = nullptr;
     float *v_host = nullptr;  // pinned: states | normalized | logits | proposals
     uint32_t *v_next = nullptr, *v_next_host = nullptr;
+    void *v_argmax = nullptr;  // argmax partials of the candidate logits
     CopyRow *copy_table = nullptr, *copy_table_host = nullptr;
     uint64_t verification_tokens = 0, verification_index = 0;
 
@@ -1204,8 +1205,10 @@ int run_prompt(plamo_metal *m, struct model *model, const uint32_t *ids, uint64_
             m->v_logits = dev_alloc<float>(m, kMaxVerify * V);
             m->v_prop = dev_alloc<float>(m, prop);
             m->v_next = dev_alloc<uint32_t>(m, kMaxVerify);
+            m->v_argmax = dev_alloc<char>(m, argmax_scratch_bytes(kMaxVerify));
             m->copy_table = dev_alloc<CopyRow>(m, 3 * kMaxLayers);
             if (!m->v_state || !m->v_norm || !m->v_logits || !m->v_prop || !m->v_next ||
+                !m->v_argmax ||
                 !m->copy_table ||
                 hipHostMalloc((void **)&m->v_host, (kMaxVerify * (2 * h + V) + prop) * 4,
                               hipHostMallocDefault) != hipSuccess ||
@@ -1219,6 +1222,14 @@ int run_prompt(plamo_metal *m, struct model *model, const uint32_t *ids, uint64_
         }
     }
     std::vector<char> overflow(L, 0);
+    uint64_t split_floats = 0;
+    for (uint64_t i = 0; i < L; ++i) {
+        const Layer &d = m->layers[i];
+        split_floats = std::max(split_floats,
+                                prompt_attention_scratch((uint32_t)model->layers[i]->mixer->cache->count,
+                                                         (uint32_t)T, d.qh, d.dim));
+    }
+    if (split_floats && !ensure(m, m->p_attn_split, split_floats * 4)) return -1;
     for (uint64_t i = 0; i < L; ++i) {
         Layer &d = m->layers[i];
         const struct cache *c = model->layers[i]->mixer->cache;
@@ -1241,6 +1252,10 @@ int run_prompt(plamo_metal *m, struct model *model, const uint32_t *ids, uint64_
     HIP_FAIL(m, launch_embed(s, m->embedding, as<uint32_t>(m->p_ids), nullptr, (uint32_t)T,
                             (uint32_t)h, state));
     ++n;
+    // A residual followed by a norm of the same rows runs as one launch; then
+    // `normed` says the next layer's input norm is already in `norm`.
+    const bool fuse_rows = h <= 8192;
+    bool normed = false, final_normed = false;
     for (uint64_t i = 0; i < L; ++i) {
         Layer &d = m->layers[i];
         const struct cache *c = model->layers[i]->mixer->cache;
@@ -1248,9 +1263,13 @@ int run_prompt(plamo_metal *m, struct model *model, const uint32_t *ids, uint64_
                        *mpost = d.norms + 3 * h, *qn = d.norms + 4 * h, *kn = qn + d.dim;
         const RopeTable &rope = m->ropes[d.rope];
         const uint64_t qkv_w = (uint64_t)(d.qh + 2 * d.kh) * d.dim, aw = (uint64_t)d.qh * d.dim;
-        HIP_FAIL(m, launch_norm_rows(s, state, h, pre, 1.0f, norm, h, h, T));
+        if (!normed) {
+            HIP_FAIL(m, launch_norm_rows(s, state, h, pre, 1.0f, norm, h, h, T));
+            ++n;
+        }
+        normed = false;
         HIP_FAIL(m, launch_gemm(s, norm, h, d.qkv, qkv_w, h, T, qkv, qkv_w, ws));
-        n += 2;
+        ++n;
         if (stale[i] && (verify || !overflow[i])) {
             HIP_FAIL(m, launch_rerotate(s, d.k, d.rot, rope.table, c->count, d.kh, d.dim));
             d.verify_stale = verify;
@@ -1301,6 +1320,7 @@ int run_prompt(plamo_metal *m, struct model *model, const uint32_t *ids, uint64_
         pa.out = attn;
         pa.prefix = (uint32_t)c->count;
         pa.tokens = (uint32_t)T;
+        pa.partial = split_floats ? as<float>(m->p_attn_split) : nullptr;
         pa.qh = d.qh;
         pa.kh = d.kh;
         pa.dim = d.dim;
@@ -1353,20 +1373,37 @@ int run_prompt(plamo_metal *m, struct model *model, const uint32_t *ids, uint64_
             n += 5;
         } else {
             HIP_FAIL(m, launch_gemm(s, attn + first * aw, aw, d.o, h, aw, rows, branch, h, ws));
-            HIP_FAIL(m, launch_residual_rows(s, st, branch, post, kAttentionOffset, h, rows));
-            HIP_FAIL(m, launch_norm_rows(s, st, h, mpre, 1.0f, norm, h, h, rows));
+            if (fuse_rows) {
+                HIP_FAIL(m, launch_residual_norm_rows(s, st, branch, post, kAttentionOffset, mpre,
+                                                     1.0f, norm, h, h, rows));
+            } else {
+                HIP_FAIL(m, launch_residual_rows(s, st, branch, post, kAttentionOffset, h, rows));
+                HIP_FAIL(m, launch_norm_rows(s, st, h, mpre, 1.0f, norm, h, h, rows));
+                ++n;
+            }
             HIP_FAIL(m, launch_gemm(s, norm, h, d.gu, 2 * (uint64_t)d.inter, h, rows, gu,
                                    2 * (uint64_t)d.inter, ws));
             HIP_FAIL(m, launch_swiglu_rows(s, gu, act, d.inter, rows));
             HIP_FAIL(m, launch_gemm(s, act, d.inter, d.down, h, d.inter, rows, branch, h, ws));
-            HIP_FAIL(m, launch_residual_rows(s, st, branch, mpost, kMlpOffset, h, rows));
-            n += 7;
+            if (fuse_rows && i + 1 < L) {
+                HIP_FAIL(m, launch_residual_norm_rows(s, st, branch, mpost, kMlpOffset,
+                                                     m->layers[i + 1].norms, 1.0f, norm, h, h,
+                                                     rows));
+                normed = true;
+            } else if (fuse_rows && verify) {
+                HIP_FAIL(m, launch_residual_norm_rows(s, st, branch, mpost, kMlpOffset,
+                                                     m->final_norm, 1.0f, m->v_norm, h, h, rows));
+                final_normed = true;
+            } else {
+                HIP_FAIL(m, launch_residual_rows(s, st, branch, mpost, kMlpOffset, h, rows));
+            }
+            n += 6;
         }
     }
     if (verify) {
-        HIP_FAIL(m, launch_norm_rows(s, state, h, m->final_norm, 1.0f, m->v_norm, h, h, T));
+        if (!final_normed) HIP_FAIL(m, launch_norm_rows(s, state, h, m->final_norm, 1.0f, m->v_norm, h, h, T));
         HIP_FAIL(m, launch_gemm(s, m->v_norm, h, m->head, V, h, T, m->v_logits, V, ws));
-        HIP_FAIL(m, launch_argmax_rows(s, m->v_logits, V, T, m->v_next));
+        HIP_FAIL(m, launch_argmax_rows(s, m->v_logits, V, T, m->v_next, m->v_argmax));
         HIP_FAIL(m, hipMemcpyAsync(m->v_state, state, T * h * 4, hipMemcpyDeviceToDevice, s));
         HIP_FAIL(m, hipMemcpyAsync(m->v_host, m->v_state, T * h * 4, hipMemcpyDeviceToHost, s));
         HIP_FAIL(m, hipMemcpyAsync(m->v_host + kMaxVerify * h, m->v_norm, T * h * 4,

@@ -87,6 +87,12 @@ hipError_t launch_gemm(hipStream_t, const float *x, uint64_t x_stride, const uin
 hipError_t launch_norm_rows(hipStream_t, const float *x, uint64_t x_stride, const uint16_t *w,
                             float offset, float *y, uint64_t y_stride, uint64_t width,
                             uint64_t rows);
+// launch_residual_rows followed by launch_norm_rows of the updated rows into
+// norm, in one launch (width <= 8192; hipErrorInvalidValue otherwise).
+hipError_t launch_residual_norm_rows(hipStream_t, float *state, const float *branch,
+                                     const uint16_t *wr, float off_r, const uint16_t *wn,
+                                     float off_n, float *norm, uint64_t norm_stride,
+                                     uint64_t width, uint64_t rows);
 hipError_t launch_residual_rows(hipStream_t, float *state, const float *branch,
                                 const uint16_t *w, float offset, uint64_t width, uint64_t rows);
 hipError_t launch_swiglu_rows(hipStream_t, const float *gate_up, float *out,
@@ -190,8 +196,13 @@ struct PromptAttention {
     const float *table;
     float *out;              // [tokens, qh*dim]
     uint32_t prefix, tokens, qh, kh, dim, window;
+    // Optional scratch for key splits (prompt_attention_scratch floats): few
+    // query tiles then spread their keys over several blocks and a merge.
+    float *partial;
 };
 hipError_t launch_prompt_attention(hipStream_t, const PromptAttention &);
+// Floats of split scratch launch_prompt_attention uses for this shape (0: none).
+uint64_t prompt_attention_scratch(uint32_t prefix, uint32_t tokens, uint32_t qh, uint32_t dim);
 
 // Rotates cache rows [0, rows) of raw K into rotated K at their row position.
 hipError_t launch_rerotate(hipStream_t, const float *k_raw, float *k_rot, const float *table,
@@ -211,8 +222,10 @@ struct CopyRow {
 hipError_t launch_copy_rows(hipStream_t, const CopyRow *table, uint32_t entries);
 // Raises the dynamic LDS limit of the GEMV variants to hold `cols` floats.
 hipError_t configure_gemv(uint64_t max_cols);
-// First maximal index per row (strict >); any NaN gives 0xffffffff.
+// First maximal index per row (strict >); any NaN gives 0xffffffff. scratch:
+// argmax_scratch_bytes(rows) of device memory.
 hipError_t launch_argmax_rows(hipStream_t, const float *x, uint64_t width, uint64_t rows,
-                              uint32_t *out);
+                              uint32_t *out, void *scratch);
+uint64_t argmax_scratch_bytes(uint64_t rows);
 
 }  // namespace plamo

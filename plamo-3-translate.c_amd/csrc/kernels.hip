@@ -1576,6 +1576,76 @@ __global__ __launch_bounds__(kThreads) void residual_rows_kernel(float *state, c
     }
 }
 
+// Residual then the next norm of the same rows, with the row in registers:
+// state += rms(branch) * (bf16(wr) + off_r); norm = rms(state) * (bf16(wn) +
+// off_n). One block per row; element i of the row lives in thread i % 256.
+template <int NE>
+__global__ __launch_bounds__(kThreads) void residual_norm_rows_kernel(
+    float *state, const float *branch, const uint16_t *wr, float off_r, const uint16_t *wn,
+    float off_n, float *norm, uint64_t norm_stride, uint32_t width) {
+    __shared__ float red[4];
+    const uint64_t row = blockIdx.x;
+    float b[NE], st[NE];
+    uint16_t gr[NE], gn[NE];
+    // Unconditional loads at a clamped index (a guarded load would become a
+    // branch with a full wait per element), then a select.
+#pragma unroll
+    for (int j = 0; j < NE; ++j) {
+        const uint32_t i = threadIdx.x + kThreads * j;
+        const uint32_t c = i < width ? i : width - 1;
+        const bool in = i < width;
+        const float bv = branch[row * width + c], sv = state[row * width + c];
+        const uint16_t rv = wr[c], nv = wn[c];
+        b[j] = in ? bv : 0.0f;
+        st[j] = in ? sv : 0.0f;
+        gr[j] = in ? rv : 0;
+        gn[j] = in ? nv : 0;
+    }
+    float ss = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NE; ++j) {
+        const float t = b[j] * b[j];
+        ss = ss + t;
+    }
+    const float inv = block_inverse_from_partial(ss, width, red);
+    float ss2 = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NE; ++j) {
+        const uint32_t i = threadIdx.x + kThreads * j;
+        const float v = (b[j] * inv) * (bf16f(gr[j]) + off_r);
+        st[j] = st[j] + v;
+        if (i < width) state[row * width + i] = st[j];
+        const float t = st[j] * st[j];
+        ss2 = ss2 + t;
+    }
+    const float inv2 = block_inverse_from_partial(ss2, width, red);
+#pragma unroll
+    for (int j = 0; j < NE; ++j) {
+        const uint32_t i = threadIdx.x + kThreads * j;
+        if (i < width) norm[row * norm_stride + i] = (st[j] * inv2) * (bf16f(gn[j]) + off_n);
+    }
+}
+
+hipError_t launch_residual_norm_rows(hipStream_t stream, float *state, const float *branch,
+                                     const uint16_t *wr, float off_r, const uint16_t *wn,
+                                     float off_n, float *norm, uint64_t norm_stride,
+                                     uint64_t width, uint64_t rows) {
+    if (!rows) return hipSuccess;
+    const uint32_t w = (uint32_t)width;
+    if (width <= 2048)
+        residual_norm_rows_kernel<8><<<(unsigned)rows, kThreads, 0, stream>>>(
+            state, branch, wr, off_r, wn, off_n, norm, norm_stride, w);
+    else if (width <= 4096)
+        residual_norm_rows_kernel<16><<<(unsigned)rows, kThreads, 0, stream>>>(
+            state, branch, wr, off_r, wn, off_n, norm, norm_stride, w);
+    else if (width <= 8192)
+        residual_norm_rows_kernel<32><<<(unsigned)rows, kThreads, 0, stream>>>(
+            state, branch, wr, off_r, wn, off_n, norm, norm_stride, w);
+    else
+        return hipErrorInvalidValue;
+    return hipGetLastError();
+}
+
 hipError_t launch_residual_rows(hipStream_t stream, float *state, const float *branch,
                                 const uint16_t *w, float offset, uint64_t width, uint64_t rows) {
     if (!rows) return hipSuccess;
@@ -2406,7 +2476,8 @@ hipError_t launch_layer(hipStream_t stream, const LayerStep &l) {
 // its position inside the query's window, as the CPU path does after every
 // shift (src/cache_rope.s:15-27 rotates all rows at local positions).
 constexpr int kQT = 16, kKT = 32;
-__global__ __launch_bounds__(kThreads) void prompt_attention_kernel(PromptAttention a) {
+__global__ __launch_bounds__(kThreads) void prompt_attention_kernel(PromptAttention a,
+                                                                    uint32_t split_rows) {
     extern __shared__ float smem[];
     const uint32_t dim = a.dim, half = dim / 2, width = a.kh * dim;
     float *qs = smem;                    // [kQT][dim]
@@ -2419,18 +2490,35 @@ __global__ __launch_bounds__(kThreads) void prompt_attention_kernel(PromptAttent
     const uint32_t h = blockIdx.x, kvh = h / (a.qh / a.kh);
     const uint32_t t0 = blockIdx.y * kQT;
     const uint32_t nq = a.tokens - t0 < (uint32_t)kQT ? a.tokens - t0 : kQT;
-    for (uint32_t i = threadIdx.x; i < kQT * dim; i += kThreads) {
-        uint32_t q = i / dim, d = i % dim;
-        qs[i] = q < nq ? a.q[(uint64_t)(t0 + q) * a.qh * dim + (uint64_t)h * dim + d] : 0.0f;
+    // Staging loads are unconditional at clamped indices, eight per thread in
+    // flight, then selected: a guarded load would wait for each element.
+    for (uint32_t base = threadIdx.x; base < kQT * dim; base += 8 * kThreads) {
+        float v[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const uint32_t i = min(base + j * kThreads, kQT * dim - 1);
+            const uint32_t q = min(i / dim, nq - 1), d = i % dim;
+            v[j] = a.q[(uint64_t)(t0 + q) * a.qh * dim + (uint64_t)h * dim + d];
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const uint32_t i = base + j * kThreads;
+            if (i < kQT * dim) qs[i] = i / dim < nq ? v[j] : 0.0f;
+        }
     }
     if (threadIdx.x < kQT) {
         mrow[threadIdx.x] = -__builtin_inff();
         lrow[threadIdx.x] = 0.0f;
     }
-    // Key range of the block: virtual rows [lo_min, hi_max).
-    const uint32_t hi_max = a.prefix + t0 + nq;
+    // Key range of the block: virtual rows [lo_min, hi_max), cut to its split
+    // [z * split_rows, (z + 1) * split_rows) when keys are split.
+    uint32_t hi_max = a.prefix + t0 + nq;
     uint32_t lo_min = 0;
     if (a.window && a.prefix + t0 + 1 > a.window) lo_min = a.prefix + t0 + 1 - a.window;
+    if (split_rows) {
+        lo_min = max(lo_min, blockIdx.z * split_rows);
+        hi_max = min(hi_max, (blockIdx.z + 1) * split_rows);
+    }
     const float scale = 1.0f / __builtin_sqrtf((float)dim);
     // Output ownership: thread -> query tid/16, dims (tid%16) + 16*i.
     const uint32_t oq = threadIdx.x / 16, od = threadIdx.x % 16;
@@ -2440,20 +2528,28 @@ __global__ __launch_bounds__(kThreads) void prompt_attention_kernel(PromptAttent
     __syncthreads();
     for (uint32_t k0 = lo_min; k0 < hi_max; k0 += kKT) {
         const uint32_t nk = hi_max - k0 < (uint32_t)kKT ? hi_max - k0 : kKT;
-        for (uint32_t i = threadIdx.x; i < kKT * dim; i += kThreads) {
-            uint32_t r = i / dim, d = i % dim;
-            float kvv = 0.0f, vvv = 0.0f;
-            if (r < nk) {
-                uint32_t vrow = k0 + r;
+        for (uint32_t base = threadIdx.x; base < kKT * dim; base += 8 * kThreads) {
+            float kv8[8], vv8[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const uint32_t i = min(base + j * kThreads, kKT * dim - 1);
+                const uint32_t r = min(i / dim, nk - 1), d = i % dim;
+                const uint32_t vrow = k0 + r;
                 const float *kp = vrow < a.prefix ? a.k_cache + (uint64_t)vrow * width
                                                   : a.k_new + (uint64_t)(vrow - a.prefix) * width;
                 const float *vp = vrow < a.prefix ? a.v_cache + (uint64_t)vrow * width
                                                   : a.v_new + (uint64_t)(vrow - a.prefix) * width;
-                kvv = kp[(uint64_t)kvh * dim + d];
-                vvv = vp[(uint64_t)kvh * dim + d];
+                kv8[j] = kp[(uint64_t)kvh * dim + d];
+                vv8[j] = vp[(uint64_t)kvh * dim + d];
             }
-            ks[r * (dim + 1) + d] = kvv;
-            vs[r * dim + d] = vvv;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const uint32_t i = base + j * kThreads;
+                if (i >= kKT * dim) continue;
+                const uint32_t r = i / dim, d = i % dim;
+                ks[r * (dim + 1) + d] = r < nk ? kv8[j] : 0.0f;
+                vs[r * dim + d] = r < nk ? vv8[j] : 0.0f;
+            }
         }
         __syncthreads();
         // Scores: thread -> query tid/16, keys tid%16 and tid%16 + 16.
@@ -2531,6 +2627,19 @@ __global__ __launch_bounds__(kThreads) void prompt_attention_kernel(PromptAttent
         __syncthreads();
     }
     if (oq < nq) {
+        if (split_rows) {
+            // Record [split][token][head]: unnormalized output, running max, sum.
+            float *rec = a.partial +
+                         (((uint64_t)blockIdx.z * a.tokens + t0 + oq) * a.qh + h) * (dim + 2);
+#pragma unroll
+            for (int i = 0; i < 16; ++i)
+                if (i * 16 + od < dim) rec[i * 16 + od] = o[i];
+            if (od == 0) {
+                rec[dim] = mrow[oq];
+                rec[dim + 1] = lrow[oq];
+            }
+            return;
+        }
         float l = lrow[oq];
         float *out = a.out + (uint64_t)(t0 + oq) * a.qh * dim + (uint64_t)h * dim;
 #pragma unroll
@@ -2539,11 +2648,66 @@ __global__ __launch_bounds__(kThreads) void prompt_attention_kernel(PromptAttent
     }
 }
 
+// One block per (token, head): rescales each split's record to the common
+// maximum and normalizes by the combined sum. Splits with no visible key
+// carry a -inf maximum and contribute nothing.
+__global__ __launch_bounds__(128) void attention_merge_kernel(const float *partial,
+                                                              uint32_t splits, uint64_t stride,
+                                                              uint32_t dim, float *out) {
+    const float *p = partial + (uint64_t)blockIdx.x * (dim + 2);
+    float m = -__builtin_inff();
+    for (uint32_t z = 0; z < splits; ++z) m = fmaxf(m, p[z * stride + dim]);
+    float l = 0.0f;
+    for (uint32_t z = 0; z < splits; ++z) {
+        const float mz = p[z * stride + dim];
+        if (mz != -__builtin_inff()) l += p[z * stride + dim + 1] * plamo_exp(mz - m);
+    }
+    for (uint32_t d = threadIdx.x; d < dim; d += 128) {
+        float acc = 0.0f;
+        for (uint32_t z = 0; z < splits; ++z) {
+            const float mz = p[z * stride + dim];
+            if (mz != -__builtin_inff()) acc += p[z * stride + d] * plamo_exp(mz - m);
+        }
+        out[(uint64_t)blockIdx.x * dim + d] = acc / l;
+    }
+}
+
+// Key splits: only when the query tiles alone leave the GPU mostly idle;
+// splits of at least two key tiles, at most 64, within the scratch bound.
+constexpr uint64_t kAttentionScratchFloats = 8ull << 20;
+static uint32_t prompt_attention_splits(uint32_t prefix, uint32_t tokens, uint32_t qh,
+                                        uint32_t dim, uint32_t *split_rows) {
+    const uint32_t tiles = (tokens + kQT - 1) / kQT, keys = prefix + tokens;
+    const uint32_t blocks = qh * tiles;
+    *split_rows = 0;
+    if (blocks >= 256 || keys <= 2 * kKT) return 1;
+    uint32_t splits = (512 + blocks - 1) / blocks;
+    splits = min(splits, min(64u, (keys + 2 * kKT - 1) / (2 * kKT)));
+    while (splits > 1 && (uint64_t)splits * tokens * qh * (dim + 2) > kAttentionScratchFloats)
+        --splits;
+    if (splits <= 1) return 1;
+    uint32_t rows = (keys + splits - 1) / splits;
+    rows = (rows + kKT - 1) / kKT * kKT;
+    *split_rows = rows;
+    return (keys + rows - 1) / rows;
+}
+
+uint64_t prompt_attention_scratch(uint32_t prefix, uint32_t tokens, uint32_t qh, uint32_t dim) {
+    uint32_t rows;
+    const uint32_t splits = prompt_attention_splits(prefix, tokens, qh, dim, &rows);
+    return splits > 1 ? (uint64_t)splits * tokens * qh * (dim + 2) : 0;
+}
+
 hipError_t launch_prompt_attention(hipStream_t stream, const PromptAttention &a) {
     if (!a.tokens) return hipSuccess;
     size_t lds = (kQT * a.dim + kKT * (a.dim + 1) + kKT * a.dim + kQT * kKT + 3 * kQT) * sizeof(float);
-    dim3 grid(a.qh, (a.tokens + kQT - 1) / kQT);
-    prompt_attention_kernel<<<grid, kThreads, lds, stream>>>(a);
+    uint32_t rows = 0;
+    uint32_t splits = a.partial ? prompt_attention_splits(a.prefix, a.tokens, a.qh, a.dim, &rows) : 1;
+    dim3 grid(a.qh, (a.tokens + kQT - 1) / kQT, splits);
+    prompt_attention_kernel<<<grid, kThreads, lds, stream>>>(a, splits > 1 ? rows : 0);
+    if (splits > 1)
+        attention_merge_kernel<<<a.tokens * a.qh, 128, 0, stream>>>(
+            a.partial, splits, (uint64_t)a.tokens * a.qh * (a.dim + 2), a.dim, a.out);
     return hipGetLastError();
 }
 
@@ -2634,58 +2798,99 @@ hipError_t launch_copy_rows(hipStream_t stream, const CopyRow *table, uint32_t e
 
 // ---------------------------------------------------------------- argmax
 // src/token.s:37-63: first maximal index; NaN anywhere gives 0xffffffff.
-__global__ __launch_bounds__(kThreads) void argmax_kernel(const float *x, uint64_t width,
-                                                          uint32_t *out) {
+// First maximal index of each row (strict >, ties to the lower index); a row
+// holding any NaN gives 0xffffffff. Rows are split over kArgmaxChunks blocks:
+// each writes (maximum, index, NaN seen) of its chunk, then one wave per row
+// combines the chunks in index order.
+constexpr uint32_t kArgmaxChunks = 64;
+struct ArgmaxPart {
+    float best;
+    uint32_t index;  // 0xffffffff: the chunk holds no number
+    uint32_t nan;
+};
+
+__device__ __forceinline__ void argmax_take(float &best, uint32_t &index, float v, uint32_t i) {
+    if (i != 0xffffffffu && (index == 0xffffffffu || v > best || (v == best && i < index))) {
+        best = v;
+        index = i;
+    }
+}
+
+__global__ __launch_bounds__(kThreads) void argmax_chunk_kernel(const float *x, uint64_t width,
+                                                                ArgmaxPart *part) {
     __shared__ float bv[4];
-    __shared__ uint32_t bi[4];
-    __shared__ int bnan[4];
+    __shared__ uint32_t bi[4], bn[4];
     const float *row = x + (uint64_t)blockIdx.x * width;
+    const uint64_t chunk = (width + kArgmaxChunks - 1) / kArgmaxChunks;
+    const uint64_t lo = blockIdx.y * chunk, hi = min(width, lo + chunk);
     float best = -__builtin_inff();
-    uint32_t index = 0xffffffffu;
-    int nan = 0;
-    for (uint64_t i = threadIdx.x; i < width; i += kThreads) {
-        float v = row[i];
-        if (v != v) nan = 1;
-        else if (index == 0xffffffffu || v > best) {
-            best = v;
-            index = (uint32_t)i;
+    uint32_t index = 0xffffffffu, nan = 0;
+    // Four loads in flight per thread; each thread visits its indices in
+    // increasing order, so strict > keeps the first maximum.
+    for (uint64_t base = lo + threadIdx.x; base < hi; base += 4 * kThreads) {
+        float v[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint64_t i = base + (uint64_t)j * kThreads;
+            v[j] = i < hi ? row[i] : 0.0f;
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint64_t i = base + (uint64_t)j * kThreads;
+            if (i >= hi) continue;
+            if (v[j] != v[j]) nan = 1;
+            else if (index == 0xffffffffu || v[j] > best) {
+                best = v[j];
+                index = (uint32_t)i;
+            }
         }
     }
     for (int o = 32; o > 0; o >>= 1) {
-        float ov = __shfl_xor(best, o, 64);
-        uint32_t oi = __shfl_xor(index, o, 64);
+        const float ov = __shfl_xor(best, o, 64);
+        const uint32_t oi = __shfl_xor(index, o, 64);
         nan |= __shfl_xor(nan, o, 64);
-        if (oi != 0xffffffffu && (index == 0xffffffffu || ov > best || (ov == best && oi < index))) {
-            best = ov;
-            index = oi;
-        }
+        argmax_take(best, index, ov, oi);
     }
     const uint32_t wave = threadIdx.x >> 6;
     if ((threadIdx.x & 63) == 0) {
         bv[wave] = best;
         bi[wave] = index;
-        bnan[wave] = nan;
+        bn[wave] = nan;
     }
     __syncthreads();
     if (threadIdx.x == 0) {
         float b = bv[0];
-        uint32_t id = bi[0];
-        int any = bnan[0];
+        uint32_t id = bi[0], any = bn[0];
         for (int w = 1; w < 4; ++w) {
-            any |= bnan[w];
-            if (bi[w] != 0xffffffffu && (id == 0xffffffffu || bv[w] > b || (bv[w] == b && bi[w] < id))) {
-                b = bv[w];
-                id = bi[w];
-            }
+            any |= bn[w];
+            argmax_take(b, id, bv[w], bi[w]);
         }
-        out[blockIdx.x] = any ? 0xffffffffu : id;
+        part[(uint64_t)blockIdx.x * kArgmaxChunks + blockIdx.y] = ArgmaxPart{b, id, any};
     }
 }
 
+__global__ __launch_bounds__(64) void argmax_merge_kernel(const ArgmaxPart *part, uint32_t *out) {
+    const ArgmaxPart p = part[(uint64_t)blockIdx.x * kArgmaxChunks + threadIdx.x];
+    float best = p.best;
+    uint32_t index = p.index, nan = p.nan;
+    for (int o = 32; o > 0; o >>= 1) {
+        const float ov = __shfl_xor(best, o, 64);
+        const uint32_t oi = __shfl_xor(index, o, 64);
+        nan |= __shfl_xor(nan, o, 64);
+        argmax_take(best, index, ov, oi);
+    }
+    if (threadIdx.x == 0) out[blockIdx.x] = nan ? 0xffffffffu : index;
+}
+
+uint64_t argmax_scratch_bytes(uint64_t rows) { return rows * kArgmaxChunks * sizeof(ArgmaxPart); }
+
 hipError_t launch_argmax_rows(hipStream_t stream, const float *x, uint64_t width, uint64_t rows,
-                              uint32_t *out) {
+                              uint32_t *out, void *scratch) {
     if (!rows) return hipSuccess;
-    argmax_kernel<<<(unsigned)rows, kThreads, 0, stream>>>(x, width, out);
+    ArgmaxPart *part = (ArgmaxPart *)scratch;
+    argmax_chunk_kernel<<<dim3((unsigned)rows, kArgmaxChunks), kThreads, 0, stream>>>(x, width,
+                                                                                     part);
+    argmax_merge_kernel<<<(unsigned)rows, 64, 0, stream>>>(part, out);
     return hipGetLastError();
 }
 
