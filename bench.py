@@ -299,13 +299,13 @@ def main() -> int:
     ttft = {}
     for n in [int(x) for x in args.ttft_sizes.split(",") if x]:
         times = []
-        for _ in range(4):
+        for _ in range(8):
             start = time.perf_counter()
             restore(inst, snap, PREFIX)
             if be.prefill(inst, prompt[PREFIX:n]) != 1:
                 raise RuntimeError(be.info().note.decode())
             times.append(time.perf_counter() - start)
-        ttft[n] = float(np.median(times[1:])) * 1e3
+        ttft[n] = float(np.median(times[2:])) * 1e3
         log(f"TTFT {n} tokens: {ttft[n]:.2f} ms (runs {[round(t * 1e3, 2) for t in times]})")
 
     # Decode: prompt of args.prompt tokens, then greedy steps.

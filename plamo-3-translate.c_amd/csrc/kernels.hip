@@ -698,21 +698,28 @@ __global__ __launch_bounds__(kThreads) void gemv_reg_kernel(const uint16_t *__re
 // rows per step; with SWIGLU the step is the pair (gate row p, up row
 // p + half) and the output silu(gate) * up (tests/activation_reference.s:99-126).
 // The first rows' weights are requested before the prologue's reductions.
-template <int KC, int U, bool SWIGLU>
+template <int KC, int U, bool SWIGLU, int WPR = 1>
 __device__ __forceinline__ void regp_block(const uint16_t *__restrict__ w, uint64_t rows,
                                            uint64_t cols, const Prologue &pro,
                                            float *__restrict__ y, uint64_t half, uint32_t bid,
                                            uint32_t nblocks, const Gate &gate,
                                            const Signal &sig) {
     static_assert(!SWIGLU || U == 2, "a SwiGLU step is one gate/up row pair");
+    // WPR waves share a step, each holding KC of the row's KC * WPR chunks;
+    // their sums meet in LDS.
+    constexpr int GROUPS = 4 / WPR;
     extern __shared__ float xs[];
     __shared__ float red[4];
+    __shared__ float part[4][U];
     const bool through = sig.counter != nullptr;
     const uint32_t n = (uint32_t)cols;
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t pidx = wave % WPR, grp = wave / WPR;
+    const uint64_t col0 = (uint64_t)pidx * KC * 512 + lane * 8;
     const uint64_t units = SWIGLU ? half : (rows + U - 1) / U;
-    const uint64_t step = (uint64_t)nblocks * 4;
-    const uint64_t u0 = (uint64_t)bid * 4 + wave;
+    const uint64_t step = (uint64_t)nblocks * GROUPS;
+    const uint64_t ubase = (uint64_t)bid * GROUPS;
+    const uint64_t u0 = ubase + grp;
     ProloguePart pp;
     prologue_begin(pro, n, pp);
     if (!gate.counter) prologue_load(pro, pp);
@@ -723,7 +730,7 @@ __device__ __forceinline__ void regp_block(const uint16_t *__restrict__ w, uint6
         for (int u = 0; u < U; ++u) {
             uint64_t r = SWIGLU ? unit + u * half : unit * U + u;
             if (r >= rows) r = rows - 1;
-            const u32x4 *p = (const u32x4 *)(w + r * cols + lane * 8);
+            const u32x4 *p = (const u32x4 *)(w + r * cols + col0);
 #pragma unroll
             for (int c = 0; c < KC; ++c) wv[u][c] = __builtin_nontemporal_load(p + c * 64);
         }
@@ -739,13 +746,16 @@ __device__ __forceinline__ void regp_block(const uint16_t *__restrict__ w, uint6
     float x[KC][8];
 #pragma unroll
     for (int c = 0; c < KC; ++c) {
-        const f32x4 a = *(const f32x4 *)(xs + c * 512 + lane * 8);
-        const f32x4 b = *(const f32x4 *)(xs + c * 512 + lane * 8 + 4);
+        const f32x4 a = *(const f32x4 *)(xs + col0 + c * 512);
+        const f32x4 b = *(const f32x4 *)(xs + col0 + c * 512 + 4);
         x[c][0] = a.x; x[c][1] = a.y; x[c][2] = a.z; x[c][3] = a.w;
         x[c][4] = b.x; x[c][5] = b.y; x[c][6] = b.z; x[c][7] = b.w;
     }
-    for (uint64_t unit = u0; unit < units; unit += step) {
-        if (unit != u0) load(unit);
+    // With WPR > 1 every wave of the block runs every trip (barriers inside).
+    for (uint64_t ub = ubase; WPR == 1 ? ub + grp < units : ub < units; ub += step) {
+        const uint64_t unit = ub + grp;
+        const bool valid = unit < units;
+        if (ub != ubase && valid) load(unit);
         float acc[U];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
@@ -761,7 +771,21 @@ __device__ __forceinline__ void regp_block(const uint16_t *__restrict__ w, uint6
             }
             acc[u] = ok ? wave_sum(a) : __builtin_nanf("");
         }
-        if (lane == 0) {
+        if (WPR > 1) {
+            if (lane == 0)
+#pragma unroll
+                for (int u = 0; u < U; ++u) part[wave][u] = acc[u];
+            __syncthreads();
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                float t = part[grp * WPR][u];
+#pragma unroll
+                for (int q = 1; q < WPR; ++q) t += part[grp * WPR + q][u];
+                acc[u] = t;
+            }
+            __syncthreads();
+        }
+        if (lane == 0 && pidx == 0 && valid) {
             if (SWIGLU) {
                 const float d = plamo_exp(-acc[0]) + 1.0f;
                 put(y + unit, (acc[0] / d) * acc[1], through);
@@ -775,13 +799,13 @@ __device__ __forceinline__ void regp_block(const uint16_t *__restrict__ w, uint6
     signal_done(sig, bid);
 }
 
-template <int KC, int U, bool SWIGLU>
+template <int KC, int U, bool SWIGLU, int WPR = 1>
 __global__ __launch_bounds__(kThreads) void gemv_regp_kernel(const uint16_t *__restrict__ w,
                                                              uint64_t rows, uint64_t cols,
                                                              Prologue pro, float *__restrict__ y,
                                                              uint64_t half) {
-    regp_block<KC, U, SWIGLU>(w, rows, cols, pro, y, half, blockIdx.x, gridDim.x, Gate{},
-                              Signal{});
+    regp_block<KC, U, SWIGLU, WPR>(w, rows, cols, pro, y, half, blockIdx.x, gridDim.x, Gate{},
+                                   Signal{});
 }
 
 // Column counts the register GEMV covers: cols = 512 * KC * WPR.
@@ -840,22 +864,28 @@ static hipError_t gemv_variant(hipStream_t stream, const uint16_t *w, uint64_t r
     return hipGetLastError();
 }
 
-// Register-x prologue GEMV for widths of whole 512-column chunks. Grid: one
-// step (U rows or a gate/up pair) per wave at most; SwiGLU streams twice the
-// rows per output and takes twice the blocks.
-template <int KC>
+// Register-x prologue GEMV for widths of whole 512-column chunks (KC chunks
+// per wave, WPR waves per step). Grid: one step (U rows or a gate/up pair) per
+// wave group at most, capped at the blocks the GPU holds at once.
+template <int KC, int WPR = 1>
 static hipError_t regp_variant(hipStream_t stream, const uint16_t *w, uint64_t rows,
                                uint64_t cols, const Prologue &pro, float *y, uint64_t half,
                                int blocks_hint) {
+    constexpr int GROUPS = 4 / WPR;
     const uint64_t units = half ? half : (rows + 1) / 2;
-    uint64_t blocks = (units + 3) / 4;
-    const uint64_t cap = blocks_hint > 0 ? (uint64_t)blocks_hint * (half ? 2 : 1) : blocks;
+    uint64_t blocks = (units + GROUPS - 1) / GROUPS;
+    // blocks_hint is two blocks per CU. SwiGLU grids take more: the split-row
+    // variant exactly the three per CU it holds at once (a second, partial
+    // generation would add a tail), the others four (measured best).
+    const uint64_t cap = blocks_hint > 0
+                             ? (uint64_t)blocks_hint * (half ? (WPR > 1 ? 3 : 4) : 2) / 2
+                             : blocks;
     if (blocks > cap) blocks = cap;
     const size_t lds = cols * sizeof(float);
     if (half)
-        gemv_regp_kernel<KC, 2, true><<<(unsigned)blocks, kThreads, lds, stream>>>(w, rows, cols, pro, y, half);
+        gemv_regp_kernel<KC, 2, true, WPR><<<(unsigned)blocks, kThreads, lds, stream>>>(w, rows, cols, pro, y, half);
     else
-        gemv_regp_kernel<KC, 2, false><<<(unsigned)blocks, kThreads, lds, stream>>>(w, rows, cols, pro, y, 0);
+        gemv_regp_kernel<KC, 2, false, WPR><<<(unsigned)blocks, kThreads, lds, stream>>>(w, rows, cols, pro, y, 0);
     return hipGetLastError();
 }
 
@@ -867,7 +897,7 @@ static bool regp_launch(hipStream_t stream, const uint16_t *w, uint64_t rows, ui
     case 4: *status = regp_variant<4>(stream, w, rows, cols, pro, y, half, blocks_hint); return true;
     case 5: *status = regp_variant<5>(stream, w, rows, cols, pro, y, half, blocks_hint); return true;
     case 8: *status = regp_variant<8>(stream, w, rows, cols, pro, y, half, blocks_hint); return true;
-    case 12: *status = regp_variant<12>(stream, w, rows, cols, pro, y, half, blocks_hint); return true;
+    case 12: *status = regp_variant<6, 2>(stream, w, rows, cols, pro, y, half, blocks_hint); return true;
     default: return false;
     }
 }
