@@ -661,8 +661,10 @@ int encode_decode(plamo_metal *m, struct model *model, const DecodePlan &plan, i
             da.qkv = m->qkv;
             da.qn = qn;
             da.kn = kn;
-            da.table = rope.table;
+            da.freq = rope.freq_dev;
+            memcpy(&da.rope_scale, &rope.scale_bits, 4);
             da.k_raw = d.k;
+            da.rows = (uint32_t)d.rows;
             da.v = d.v;
             da.k_rot = d.rot;
             da.stage = plan.direct ? nullptr : layer_stage;
@@ -1740,8 +1742,10 @@ extern "C" int plamo_hip_time_kernel(struct plamo_metal *m, struct model *model,
             da.qkv = m->qkv;
             da.qn = d.norms + 4 * h;
             da.kn = d.norms + 4 * h + d.dim;
-            da.table = m->ropes[d.rope].table;
+            da.freq = m->ropes[d.rope].freq_dev;
+            memcpy(&da.rope_scale, &m->ropes[d.rope].scale_bits, 4);
             da.k_raw = d.k;
+            da.rows = (uint32_t)d.rows;
             da.v = d.v;
             da.k_rot = d.rot;
             da.stage = nullptr;

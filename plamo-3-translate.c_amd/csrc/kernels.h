@@ -126,8 +126,10 @@ hipError_t launch_qkv_post(hipStream_t, const QkvPost &);
 struct DecodeAttention {
     const float *qkv;        // [(qh+2kh)*dim] projection output
     const uint16_t *qn, *kn;
-    const float *table;      // RoPE rows [position][dim]: cos | sin
+    const float *freq;       // RoPE frequencies [dim / 2] of the layer's table
+    float rope_scale;        // and its concentration (rope_cos_sin)
     float *k_raw, *v, *k_rot;  // cache rows [rows, kh*dim]
+    uint32_t rows;           // allocated cache rows (every tile row is clamped below it)
     float *stage;            // optional [3][kh*dim] copy of the appended row
     float *host_k, *host_v, *host_rot;  // optional device views of the host cache rows
     float *out;              // [qh*dim]

@@ -210,16 +210,13 @@ __device__ float block_inverse_from_partial(float s, uint32_t n, float *red) {
 
 
 // ---------------------------------------------------------------- RoPE table
-// src/rope_table.s:5-30 with src/trig.s:5-44, evaluated per (row, j) in FP64.
-__global__ __launch_bounds__(kThreads) void rope_table_kernel(const float *freq, float scale,
-                                                              uint32_t half, uint64_t first_row,
-                                                              uint64_t rows, float *table) {
-    uint64_t e = (uint64_t)blockIdx.x * kThreads + threadIdx.x;
-    if (e >= rows * half) return;
-    uint64_t row = first_row + e / half;
-    uint32_t j = (uint32_t)(e % half);
-    float position = (float)row;
-    float angle = freq[j] * position;
+// src/rope_table.s:5-30 with src/trig.s:5-44, evaluated per (row, j) in FP64:
+// the cosine and sine of frequency j at `position`, times `scale`. The table
+// kernel and the decode attention (which rotates at the step's position
+// without a table lookup) share it, so both give the same bits.
+__device__ __forceinline__ void rope_cos_sin(float freq, float scale, float position, float &cs,
+                                             float &sn) {
+    float angle = freq * position;
     double a = (double)angle;
     const double two_pi = 6.283185307179586;
     double n = __builtin_rint(a / two_pi);
@@ -245,9 +242,19 @@ __global__ __launch_bounds__(kThreads) void rope_table_kernel(const float *freq,
     p = __builtin_fma(p, r2, -0.5);
     p = __builtin_fma(p, r2, 1.0);
     float c = (float)p;
+    cs = c * scale;
+    sn = s * scale;
+}
+
+__global__ __launch_bounds__(kThreads) void rope_table_kernel(const float *freq, float scale,
+                                                              uint32_t half, uint64_t first_row,
+                                                              uint64_t rows, float *table) {
+    uint64_t e = (uint64_t)blockIdx.x * kThreads + threadIdx.x;
+    if (e >= rows * half) return;
+    uint64_t row = first_row + e / half;
+    uint32_t j = (uint32_t)(e % half);
     float *out = table + row * 2 * half;
-    out[j] = c * scale;
-    out[half + j] = s * scale;
+    rope_cos_sin(freq[j], scale, (float)row, out[j], out[half + j]);
 }
 
 hipError_t launch_rope_table(hipStream_t stream, const float *freq, float scale, uint32_t half,
@@ -715,22 +722,25 @@ __device__ __forceinline__ void regp_block(const uint16_t *__restrict__ w, uint6
     const uint32_t n = (uint32_t)cols;
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const uint32_t pidx = wave % WPR, grp = wave / WPR;
-    const uint64_t col0 = (uint64_t)pidx * KC * 512 + lane * 8;
-    const uint64_t units = SWIGLU ? half : (rows + U - 1) / U;
-    const uint64_t step = (uint64_t)nblocks * GROUPS;
-    const uint64_t ubase = (uint64_t)bid * GROUPS;
-    const uint64_t u0 = ubase + grp;
+    // Unit (row or row pair) indices fit 32 bits (the launcher checks rows);
+    // 64-bit arithmetic only forms addresses.
+    const uint32_t col0 = pidx * KC * 512 + lane * 8;
+    const uint32_t units = (uint32_t)(SWIGLU ? half : (rows + U - 1) / U);
+    const uint32_t step = nblocks * GROUPS;
+    const uint32_t ubase = bid * GROUPS;
+    const uint32_t u0 = ubase + grp;
     ProloguePart pp;
     prologue_begin(pro, n, pp);
     if (!gate.counter) prologue_load(pro, pp);
     __builtin_amdgcn_sched_barrier(0);
     u32x4 wv[U][KC];
-    auto load = [&](uint64_t unit) {
+    const uint32_t last = (uint32_t)rows - 1, uhalf = (uint32_t)half;
+    auto load = [&](uint32_t unit) {
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            uint64_t r = SWIGLU ? unit + u * half : unit * U + u;
-            if (r >= rows) r = rows - 1;
-            const u32x4 *p = (const u32x4 *)(w + r * cols + col0);
+            uint32_t r = SWIGLU ? unit + u * uhalf : unit * U + u;
+            if (r > last) r = last;
+            const u32x4 *p = (const u32x4 *)(w + (uint64_t)r * cols + col0);
 #pragma unroll
             for (int c = 0; c < KC; ++c) wv[u][c] = __builtin_nontemporal_load(p + c * 64);
         }
@@ -752,8 +762,8 @@ __device__ __forceinline__ void regp_block(const uint16_t *__restrict__ w, uint6
         x[c][4] = b.x; x[c][5] = b.y; x[c][6] = b.z; x[c][7] = b.w;
     }
     // With WPR > 1 every wave of the block runs every trip (barriers inside).
-    for (uint64_t ub = ubase; WPR == 1 ? ub + grp < units : ub < units; ub += step) {
-        const uint64_t unit = ub + grp;
+    for (uint32_t ub = ubase; WPR == 1 ? ub + grp < units : ub < units; ub += step) {
+        const uint32_t unit = ub + grp;
         const bool valid = unit < units;
         if (ub != ubase && valid) load(unit);
         float acc[U];
@@ -892,7 +902,7 @@ static hipError_t regp_variant(hipStream_t stream, const uint16_t *w, uint64_t r
 static bool regp_launch(hipStream_t stream, const uint16_t *w, uint64_t rows, uint64_t cols,
                         const Prologue &pro, float *y, uint64_t half, int blocks_hint,
                         hipError_t *status) {
-    if (!pro.w || cols % 512 || ((uintptr_t)w & 15)) return false;
+    if (!pro.w || cols % 512 || ((uintptr_t)w & 15) || rows >= (1ull << 31)) return false;
     switch (cols / 512) {
     case 4: *status = regp_variant<4>(stream, w, rows, cols, pro, y, half, blocks_hint); return true;
     case 5: *status = regp_variant<5>(stream, w, rows, cols, pro, y, half, blocks_hint); return true;
@@ -1782,11 +1792,14 @@ hipError_t launch_qkv_post(hipStream_t stream, const QkvPost &a) {
 // across blocks whose partials (max, sum, weighted values) the last block of
 // the KV head merges.
 //
-// Phase 0: the count-independent loads go out first (vector-memory loads
-// return in order): the query heads, the new key/value and their norm
-// weights; then the RoPE row of the step's position; then two passes of K and
-// V rows. The query heads are normalized and rotated into LDS while the rows
-// are in flight; the last wave normalizes, rotates and appends the new row.
+// Phase 0: every load goes out at once, none waiting for the row count: the
+// query heads, the new key/value and their norm weights, and the block's
+// fixed tile of 64 cached K and V rows (rows [64 * split, 64 * split + 64),
+// clamped to the allocation; rows at or past the count are masked once it
+// has arrived). The rotation of the step's position is evaluated in FP64 as
+// the table's rows are (no table lookup after the count). The query heads are
+// normalized and rotated into LDS while the rows are in flight; the last wave
+// normalizes, rotates and appends the new row.
 // Phase 1: scores. For each pass a wave takes RW rows, 16 lanes per row (each
 // lane DIM/16 dims), reduced with DPP; scores go to LDS [row][head].
 // Phase 2: per head (one wave each) the maximum, exp in place, and the sum.
@@ -1855,51 +1868,22 @@ __device__ __forceinline__ void attention_block(const DecodeAttention &a, uint32
         vx[1] = vsrc[hj + HALF];
     };
     if (!gate.counter) load_inputs();
+    const float freq = a.freq[hj];
 
     const uint32_t count = a.params->count[a.layer];
-    const uint32_t n = count + 1;
-    uint32_t splits = (n + kRowsPerBlock - 1) / kRowsPerBlock;
-    if (splits > a.splits) splits = a.splits;
-    if (split >= splits) return;
-    const uint32_t per = (n + splits - 1) / splits;
-    const uint32_t lo = split * per < n ? split * per : n;
-    uint32_t hi = lo + per < n ? lo + per : n;
-    if (hi - lo > kRowsPerBlock) hi = lo + kRowsPerBlock;  // the host sizes splits so this never cuts
-    const bool owner = count >= lo && count < hi;
-    // Cached rows of this block; the appended row (index count, the last one)
-    // is scored from LDS.
-    const uint32_t hr = hi < count ? hi : count;
-    const float *cs = a.table + (uint64_t)count * DIM;
-    float rc = 0.0f, rs = 0.0f;
-    if (!gate.counter) {
-        rc = cs[hj];
-        rs = cs[HALF + hj];
-    }
-
-    // Every lane loads unconditionally, also past the range (branches around
-    // loads make the compiler wait for every load in flight where paths
-    // merge); such rows are masked later. They are mirrored back into the
-    // block's rows rather than clamped to one row, which would send every
-    // such load to one memory channel.
+    const uint32_t lo = split * kRowsPerBlock;
+    const uint32_t last_row = a.rows - 1;
     const float *kbase = a.k_rot + (uint64_t)kvh * DIM;
     const float *vbase = a.v + (uint64_t)kvh * DIM;
     const uint32_t kd0 = (lane & 15) * KD, rg = lane >> 4;
-    const uint32_t span = hr > lo ? hr - lo : 0;
-    const float inv_span = span ? 1.0f / (float)span : 0.0f;
-    auto valid_row = [&](uint32_t row) -> uint32_t {
-        if (row < hr) return row;
-        if (!span) return lo;
-        // hr - 1 - ((row - hr) mod span); the float quotient is off by at most one.
-        const int past = (int)(row - hr);
-        int r = past - (int)((float)past * inv_span) * (int)span;
-        r = r < 0 ? r + (int)span : (r >= (int)span ? r - (int)span : r);
-        return hr - 1 - (uint32_t)r;
-    };
+    // Tile rows past the allocation read its last row (every address stays in
+    // bounds); whatever such rows hold is masked below.
+    auto tile_row = [&](uint32_t row) -> uint32_t { return row < last_row ? row : last_row; };
     const uint32_t voff = lane * PL * 4;
     auto load_k = [&](uint32_t base, float (&kr)[KR][KD]) {
 #pragma unroll
         for (int j = 0; j < KR; ++j) {
-            const uint32_t row = valid_row(base + rg + 4 * j);
+            const uint32_t row = tile_row(base + rg + 4 * j);
             const char *k = (const char *)(kbase + (uint64_t)row * width + kd0);
 #pragma unroll
             for (int i = 0; i < KD; i += 4) {
@@ -1914,7 +1898,7 @@ __device__ __forceinline__ void attention_block(const DecodeAttention &a, uint32
     auto load_v = [&](uint32_t base, float (&vr)[RW][PL]) {
 #pragma unroll
         for (int r = 0; r < (int)RW; ++r) {
-            const char *vp = (const char *)(vbase + (uint64_t)valid_row(base + r) * width) + voff;
+            const char *vp = (const char *)(vbase + (uint64_t)tile_row(base + r) * width) + voff;
             if (PL == 2) {
                 f32x2 x = *(const f32x2 *)vp;
                 vr[r][0] = x.x;
@@ -1933,12 +1917,21 @@ __device__ __forceinline__ void attention_block(const DecodeAttention &a, uint32
     __builtin_amdgcn_sched_barrier(0);
     load_v(base0, vc0);
     __builtin_amdgcn_sched_barrier(0);
+
+    // The tile's share of rows [0, count] (the appended row, index count, is
+    // scored from LDS); tiles past them have nothing to do.
+    const uint32_t n = count + 1;
+    if (lo >= n) return;
+    const uint32_t splits = (n + kRowsPerBlock - 1) / kRowsPerBlock;
+    const uint32_t hi = lo + kRowsPerBlock < n ? lo + kRowsPerBlock : n;
+    const bool owner = count >= lo && count < hi;
+    const uint32_t hr = hi < count ? hi : count;  // cached rows of this block
+    float rc, rs;
+    rope_cos_sin(freq, a.rope_scale, (float)count, rc, rs);
     bool ok = true;
     if (gate.counter) {
         ok = gate_wait(gate);
         load_inputs();
-        rc = cs[hj];
-        rs = cs[HALF + hj];
     }
 
     // Offset-1 head RMSNorm then split-half rotation (src/qkv.s:36-67,
@@ -2110,11 +2103,15 @@ __device__ __forceinline__ void attention_block(const DecodeAttention &a, uint32
 #pragma unroll
                 for (int g = 0; g < G; ++g) pr[g] = sc[(row - lo) * G + g];
             }
+            // Rows past the count are selected away (their memory may hold
+            // any bits, and 0 * NaN is NaN).
+            const bool live = row < hr;
 #pragma unroll
             for (int g = 0; g < G; ++g) {
-                const float p = row < hr ? pr[g] : 0.0f;
+                const float p = live ? pr[g] : 0.0f;
 #pragma unroll
-                for (int e = 0; e < PL; ++e) acc[g][e] = __builtin_fmaf(p, vc[r][e], acc[g][e]);
+                for (int e = 0; e < PL; ++e)
+                    acc[g][e] = __builtin_fmaf(p, live ? vc[r][e] : 0.0f, acc[g][e]);
             }
         }
     };
