@@ -8,6 +8,7 @@
 // them zero-copy with the GPU, runtime/metal_model.m:57-119), and host edits
 // between calls are detected and uploaded. A decode step is one hipGraph.
 #include "../../include/plamo_backend.h"
+#include "../../include/plamo_checkpoint.h"
 #include "../../include/plamo_compute.h"
 #include "../../include/plamo_diag.h"
 #include "../../include/plamo_draft.h"
@@ -236,11 +237,20 @@ const void *resolve(const plamo_metal *m, const void *host, uint64_t bytes) {
 int add_range(plamo_metal *m, const void *host, uint64_t bytes) {
     if (!host || !bytes) return 1;
     if (resolve(m, host, bytes)) return 1;
-    char *dev = dev_alloc<char>(m, bytes);
-    if (!dev) return 0;
+    // A safetensors shard keeps its tensors at offsets of its data section,
+    // which starts 8 + header-length bytes in (8-byte aligned by the format):
+    // the copy is placed so that the data section starts on a 256-byte
+    // boundary, keeping the 16-byte row alignment the vector kernels take.
+    uint64_t shift = 0;
+    struct plamo_safetensors_view view;
+    if (plamo_safetensors_view(host, bytes, &view))
+        shift = (256 - (uint64_t)((const char *)view.data - (const char *)host) % 256) % 256;
+    char *base = dev_alloc<char>(m, bytes + shift);
+    if (!base) return 0;
+    char *dev = base + shift;
     if (hipMemcpy(dev, host, bytes, hipMemcpyHostToDevice) != hipSuccess) {
         (void)hipGetLastError();
-        dev_free(m, dev);
+        dev_free(m, base);
         return problem(m, "cannot copy %llu weight bytes to HBM", (unsigned long long)bytes);
     }
     Range r{(uintptr_t)host, bytes, dev};

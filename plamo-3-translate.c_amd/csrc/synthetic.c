@@ -10,7 +10,7 @@
  * and independent of the thread count.
  */
 #define _GNU_SOURCE
-#include "../../include/plamo_synthetic.h"
+#include "layout.h"
 #include <hip/hip_runtime_api.h>
 #include <math.h>
 #include <pthread.h>
@@ -49,7 +49,6 @@ struct allocation {
 };
 
 struct plamo_synthetic_instance {
-    const struct plamo_synthetic *s;
     struct model model;
     struct layer *layer;
     struct layer **layers;
@@ -109,8 +108,8 @@ static void quantile_table(double *out) {
 }
 
 /* tools/rope_constants.py:21-52, each fp() a float rounding. */
-static void frequencies(double theta, uint64_t half, int yarn, double factor, double original,
-                        double beta_fast, double beta_slow, float *out) {
+void plamo_layout_frequencies(double theta, uint64_t half, int yarn, double factor,
+                              double original, double beta_fast, double beta_slow, float *out) {
     double low = 0, high = 0;
     if (yarn) {
         low = (double)half * log(original / (beta_fast * 2 * M_PI)) / log(theta);
@@ -239,9 +238,9 @@ struct plamo_synthetic *plamo_synthetic_build(const struct plamo_synthetic_confi
         s->weight_table[i] = to_bf16((float)(quantiles[i] * c->weight_std));
         s->embedding_table[i] = to_bf16((float)(quantiles[i] * c->embedding_std));
     }
-    frequencies(c->local_theta, c->dim / 2, 0, 0, 0, 0, 0, s->local_freq);
-    frequencies(c->global_theta, c->dim / 2, 1, c->yarn_factor, c->yarn_original,
-                c->yarn_beta_fast, c->yarn_beta_slow, s->global_freq);
+    plamo_layout_frequencies(c->local_theta, c->dim / 2, 0, 0, 0, 0, 0, s->local_freq);
+    plamo_layout_frequencies(c->global_theta, c->dim / 2, 1, c->yarn_factor, c->yarn_original,
+                             c->yarn_beta_fast, c->yarn_beta_slow, s->global_freq);
     s->local_scale = 1.0f;
     s->global_scale = (float)(1.0 + 0.1 * log(c->yarn_factor));
 
@@ -362,16 +361,18 @@ static void *allocate(struct plamo_synthetic_instance *in, uint64_t floats, int 
     return base;
 }
 
-struct plamo_synthetic_instance *plamo_synthetic_instantiate(const struct plamo_synthetic *s,
-                                                             int pinned, char *error, size_t cap) {
-    const struct plamo_synthetic_config *c = &s->config;
+static int layout_global(const struct plamo_layout *c, uint64_t layer) {
+    return c->pattern && (layer + 1) % c->pattern == 0;
+}
+
+struct plamo_synthetic_instance *plamo_layout_instantiate(const struct plamo_layout *c, int pinned,
+                                                          char *error, size_t cap) {
     uint64_t L = c->layers, h = c->hidden, d = c->dim;
     struct plamo_synthetic_instance *in = calloc(1, sizeof *in);
     if (!in) {
         snprintf(error, cap, "cannot allocate model instance");
         return NULL;
     }
-    in->s = s;
     in->capacity = 16 + 3 * L;
     in->allocations = calloc(in->capacity, sizeof *in->allocations);
     in->layer = calloc(L, sizeof *in->layer);
@@ -388,7 +389,7 @@ struct plamo_synthetic_instance *plamo_synthetic_instantiate(const struct plamo_
         goto fail;
     uint64_t max_capacity = c->window + 1;
     for (uint64_t i = 0; i < L; ++i)
-        if (is_global(c, i) && c->global_capacity > max_capacity)
+        if (layout_global(c, i) && c->global_capacity > max_capacity)
             max_capacity = c->global_capacity;
     /* Shared workspace (tools/model_layout.py:183-196). */
     float *state = allocate(in, h, pinned), *normalized = allocate(in, h, pinned);
@@ -402,22 +403,21 @@ struct plamo_synthetic_instance *plamo_synthetic_instantiate(const struct plamo_
     if (!state || !normalized || !branch || !qkvout || !attention || !mlpscratch || !scores ||
         !cos || !sin || !logits)
         goto fail;
-    const uint16_t *w = s->arena;
     struct model *m = &in->model;
-    m->embedding = w + s->embedding;
+    m->embedding = c->embedding;
     m->vocab = c->vocab;
     m->hidden = h;
     m->state = state;
     m->layers = in->layers;
     m->count = L;
     m->scales = in->scales;
-    m->norm = w + s->norm;
+    m->norm = c->norm;
     m->normalized = normalized;
-    m->head = w + s->head;
+    m->head = c->head;
     m->logits = logits;
     for (uint64_t i = 0; i < L; ++i) {
-        const struct layer_weights *lw = &s->layers[i];
-        int global = is_global(c, i);
+        const struct plamo_layout_layer *lw = &c->layer[i];
+        int global = layout_global(c, i);
         uint64_t capacity = global ? c->global_capacity : c->window + 1;
         struct cache *cache = &in->cache[i];
         cache->capacity = capacity;
@@ -429,28 +429,54 @@ struct plamo_synthetic_instance *plamo_synthetic_instantiate(const struct plamo_
         if (!cache->k || !cache->v || !rotated)
             goto fail;
         struct rotation *r = &in->rotation[i];
-        *r = (struct rotation){cache, rotated, global ? s->global_freq : s->local_freq, cos, sin,
+        *r = (struct rotation){cache, rotated, global ? c->global_freq : c->local_freq, cos, sin,
                                c->kh, d, 0, 0};
         struct qkv *q = &in->qkv[i];
-        *q = (struct qkv){normalized, w + lw->qkv, w + lw->qn, w + lw->kn, qkvout, h,
-                          c->qh, c->kh, d};
+        *q = (struct qkv){normalized, lw->qkv, lw->qn, lw->kn, qkvout, h, c->qh, c->kh, d};
         struct gqa *g = &in->gqa[i];
         *g = (struct gqa){qkvout, rotated, cache->v, attention, scores, 0, d, c->qh, c->kh};
         struct mixer *mx = &in->mixer[i];
-        *mx = (struct mixer){q, cache, r, g, w + lw->o, branch, h};
+        *mx = (struct mixer){q, cache, r, g, lw->o, branch, h};
         struct mlp *p = &in->mlp[i];
-        *p = (struct mlp){state, w + lw->mlp_pre, w + lw->mlp_post, w + lw->gu, w + lw->down,
-                          normalized, branch, mlpscratch, h, c->intermediate};
+        *p = (struct mlp){state, lw->mlp_pre, lw->mlp_post, lw->gu, lw->down, normalized, branch,
+                          mlpscratch, h, c->intermediate};
         struct layer *l = &in->layer[i];
-        *l = (struct layer){state, w + lw->pre, w + lw->post, normalized, branch, mx, p, h};
+        *l = (struct layer){state, lw->pre, lw->post, normalized, branch, mx, p, h};
         in->layers[i] = l;
-        in->scales[i] = global ? s->global_scale : s->local_scale;
+        in->scales[i] = global ? c->global_scale : c->local_scale;
     }
     return in;
 fail:
     snprintf(error, cap, "cannot allocate model instance buffers");
     plamo_synthetic_release(in);
     return NULL;
+}
+
+struct plamo_synthetic_instance *plamo_synthetic_instantiate(const struct plamo_synthetic *s,
+                                                             int pinned, char *error, size_t cap) {
+    const struct plamo_synthetic_config *c = &s->config;
+    struct plamo_layout_layer *layers = calloc(c->layers, sizeof *layers);
+    if (!layers) {
+        snprintf(error, cap, "cannot allocate model instance");
+        return NULL;
+    }
+    const uint16_t *w = s->arena;
+    for (uint64_t i = 0; i < c->layers; ++i) {
+        const struct layer_weights *lw = &s->layers[i];
+        layers[i] = (struct plamo_layout_layer){w + lw->pre,     w + lw->post,     w + lw->qkv,
+                                                w + lw->qn,      w + lw->kn,       w + lw->o,
+                                                w + lw->mlp_pre, w + lw->mlp_post, w + lw->gu,
+                                                w + lw->down};
+    }
+    struct plamo_layout lay = {c->hidden,    c->layers,         c->qh,
+                               c->kh,        c->dim,            c->intermediate,
+                               c->vocab,     c->window,         c->global_capacity,
+                               c->pattern,   w + s->embedding,  w + s->head,
+                               w + s->norm,  layers,            s->local_freq,
+                               s->global_freq, s->local_scale,  s->global_scale};
+    struct plamo_synthetic_instance *in = plamo_layout_instantiate(&lay, pinned, error, cap);
+    free(layers);
+    return in;
 }
 
 void plamo_synthetic_release(struct plamo_synthetic_instance *in) {

@@ -127,6 +127,44 @@ class SyntheticConfig(Structure):
         ("yarn_original", c_double), ("yarn_beta_fast", c_double), ("yarn_beta_slow", c_double)]
 
 
+class SafetensorsView(Structure):
+    _fields_ = [("header", c_void_p), ("header_size", c_uint64), ("data", c_void_p),
+                ("data_size", c_uint64)]
+
+
+class Number(Structure):
+    _fields_ = [("next", c_void_p), ("value", c_uint64)]
+
+
+class JsonToken(Structure):
+    _fields_ = [("next", c_void_p), ("start", c_void_p), ("length", c_uint64),
+                ("value", c_uint64)]
+
+
+class TensorField(Structure):
+    _fields_ = [("next", c_void_p), ("offset", c_uint64), ("bytes", c_uint64), ("rank", c_uint64),
+                ("dims", c_uint64 * 4)]
+
+
+class Tensor(Structure):
+    _fields_ = [("data", c_void_p), ("bytes", c_uint64), ("rank", c_uint64),
+                ("dims", c_uint64 * 4), ("reserved", c_uint64)]
+
+
+class WeightSpec(Structure):
+    _fields_ = [("name", c_char_p), ("rank", c_uint64), ("shape", POINTER(c_uint64)),
+                ("slot", POINTER(c_void_p))]
+
+
+class CheckpointConfig(Structure):
+    _fields_ = [(name, c_uint64) for name in (
+        "hidden", "layers", "qh", "kh", "dim", "intermediate", "vocab", "window", "pattern",
+        "max_positions")] + [
+        ("tied", c_int), ("local_theta", c_double), ("global_yarn", c_int),
+        ("global_theta", c_double), ("factor", c_double), ("original", c_double),
+        ("beta_fast", c_double), ("beta_slow", c_double)]
+
+
 class CpuPath(Structure):
     _fields_ = [("forward", ctypes.CFUNCTYPE(c_int, POINTER(Model), c_uint64)),
                 ("prefill", ctypes.CFUNCTYPE(c_int, POINTER(Model), POINTER(c_uint32), c_uint64,
@@ -244,6 +282,22 @@ def load() -> ctypes.CDLL:
         "plamo_synthetic_release": (None, [c_void_p]),
         "plamo_synthetic_model": (M, [c_void_p]),
         "plamo_synthetic_fill_kv": (c_int, [c_void_p, c_uint64, c_uint64]),
+        "plamo_safetensors_view": (c_int, [c_void_p, c_uint64, POINTER(SafetensorsView)]),
+        "plamo_parse_u64": (c_int, [c_void_p, c_void_p, POINTER(Number)]),
+        "plamo_json_next": (c_int, [c_void_p, c_void_p, POINTER(JsonToken)]),
+        "plamo_tensor_descriptor": (c_int, [c_void_p, c_void_p, c_uint64, POINTER(TensorField)]),
+        "plamo_find_tensor": (c_int, [c_void_p, c_uint64, c_char_p, POINTER(Tensor)]),
+        "plamo_resolve_weight": (c_void_p, [POINTER(Mapping), c_uint64, c_char_p, c_uint64,
+                                            POINTER(c_uint64)]),
+        "plamo_bind_weights": (c_int, [POINTER(Mapping), c_uint64, POINTER(WeightSpec)]),
+        "plamo_checkpoint_open": (c_void_p, [c_char_p, c_uint64, c_char_p, c_size_t]),
+        "plamo_checkpoint_close": (None, [c_void_p]),
+        "plamo_checkpoint_config": (POINTER(CheckpointConfig), [c_void_p]),
+        "plamo_checkpoint_mappings": (POINTER(Mapping), [c_void_p, POINTER(c_size_t)]),
+        "plamo_checkpoint_schema": (POINTER(WeightSpec), [c_void_p]),
+        "plamo_checkpoint_instantiate": (c_void_p, [c_void_p, c_int, c_char_p, c_size_t]),
+        "plamo_model_set_directory": (c_int, [c_char_p]),
+        "plamo_model_open": (c_int, []),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -300,6 +354,10 @@ class Synthetic:
         if not self.handle:
             raise RuntimeError(err.value.decode())
         self.mapping = lib.plamo_synthetic_weights(self.handle).contents
+        self.mappings = [self.mapping]
+
+    def _instantiate(self, pinned: bool, err) -> int:
+        return load().plamo_synthetic_instantiate(self.handle, int(pinned), err, len(err))
 
     def instance(self, pinned=False) -> "Instance":
         return Instance(self, pinned)
@@ -310,14 +368,51 @@ class Synthetic:
             self.handle = None
 
 
-class Instance:
-    """A model instance (descriptors, KV caches, outputs) over shared weights."""
+class Checkpoint:
+    """A checkpoint directory (config.json + *.safetensors shards) opened by the
+    C binder (include/plamo_checkpoint.h); instances share its mapped weights."""
 
-    def __init__(self, synthetic: Synthetic, pinned: bool):
+    def __init__(self, directory, global_capacity: int = 0):
+        lib = load()
+        err = ctypes.create_string_buffer(512)
+        self.handle = lib.plamo_checkpoint_open(str(directory).encode(), global_capacity, err, 512)
+        if not self.handle:
+            raise RuntimeError(err.value.decode())
+        self.config = lib.plamo_checkpoint_config(self.handle).contents
+        count = c_size_t(0)
+        maps = lib.plamo_checkpoint_mappings(self.handle, ctypes.byref(count))
+        self.mappings = [maps[i] for i in range(count.value)]
+
+    def schema(self):
+        """[(name, shape)] in binding order."""
+        out, spec = [], load().plamo_checkpoint_schema(self.handle)
+        i = 0
+        while spec[i].name:
+            out.append((spec[i].name.decode(), [spec[i].shape[k] for k in range(spec[i].rank)]))
+            i += 1
+        return out
+
+    def _instantiate(self, pinned: bool, err) -> int:
+        return load().plamo_checkpoint_instantiate(self.handle, int(pinned), err, len(err))
+
+    def instance(self, pinned=False) -> "Instance":
+        return Instance(self, pinned)
+
+    def close(self):
+        if self.handle:
+            load().plamo_checkpoint_close(self.handle)
+            self.handle = None
+
+
+class Instance:
+    """A model instance (descriptors, KV caches, outputs) over shared weights
+    (a Synthetic model's or a Checkpoint's)."""
+
+    def __init__(self, synthetic, pinned: bool):
         lib = load()
         err = ctypes.create_string_buffer(256)
         self.synthetic = synthetic
-        self.handle = lib.plamo_synthetic_instantiate(synthetic.handle, int(pinned), err, 256)
+        self.handle = synthetic._instantiate(pinned, err)
         if not self.handle:
             raise RuntimeError(err.value.decode())
         self.model_ptr = lib.plamo_synthetic_model(self.handle)
@@ -395,16 +490,19 @@ class Instance:
 class Backend:
     """plamo_metal_* handle (runtime/metal.h:48-88) opened over a synthetic model."""
 
-    def __init__(self, synthetic: Synthetic | None = None, memory: int = 0):
+    def __init__(self, synthetic=None, memory: int = 0):
+        """synthetic: a Synthetic model or a Checkpoint (its weight mappings are
+        made resident), or None."""
         lib = load()
         self.lib = lib
         cfg = MetalConfig()
         cfg.memory = memory
         self._maps = None
         if synthetic is not None:
-            self._maps = (Mapping * 1)(synthetic.mapping)
+            maps = synthetic.mappings
+            self._maps = (Mapping * len(maps))(*maps)
             cfg.maps = self._maps
-            cfg.count = 1
+            cfg.count = len(maps)
         err = ctypes.create_string_buffer(1024)
         self.handle = lib.plamo_metal_open(ctypes.byref(cfg), err, 1024)
         if not self.handle:
