@@ -898,6 +898,7 @@ const GemmWorkspace *gemm_workspace(plamo_metal *m, uint64_t tokens, uint64_t co
         m->gemm.partial_floats = kGemmPartialFloats;
         m->gemm.counter_base = counters;
         m->gemm.counters = kGemmCounters;
+        m->gemm.cus = (uint32_t)m->cus;
     }
     const uint64_t need = gemm_plane_elems(std::max<uint64_t>(tokens, 128), cols);
     if (need > m->gemm.plane_elems) {
@@ -1393,9 +1394,7 @@ int run_prompt(plamo_metal *m, struct model *model, const uint32_t *ids, uint64_
                 HIP_FAIL(m, launch_norm_rows(s, st, h, mpre, 1.0f, norm, h, h, rows));
                 ++n;
             }
-            HIP_FAIL(m, launch_gemm(s, norm, h, d.gu, 2 * (uint64_t)d.inter, h, rows, gu,
-                                   2 * (uint64_t)d.inter, ws));
-            HIP_FAIL(m, launch_swiglu_rows(s, gu, act, d.inter, rows));
+            HIP_FAIL(m, launch_gemm_swiglu(s, norm, h, d.gu, d.inter, h, rows, act, gu, ws));
             HIP_FAIL(m, launch_gemm(s, act, d.inter, d.down, h, d.inter, rows, branch, h, ws));
             if (fuse_rows && i + 1 < L) {
                 HIP_FAIL(m, launch_residual_norm_rows(s, st, branch, mpost, kMlpOffset,
@@ -1688,8 +1687,7 @@ int plamo_metal_mlp(struct plamo_metal *m, const struct mlp *mlp, float *states,
          hipMemcpyAsync(st.ptr, states, T * h * 4, hipMemcpyHostToDevice, s) == hipSuccess;
     if (ok) begin_timing(m);
     ok = ok && launch_norm_rows(s, as<float>(st), h, as<uint16_t>(norms), 1.0f, as<float>(nrm), h, h, T) == hipSuccess &&
-         launch_gemm(s, as<float>(nrm), h, gu, 2 * I, h, T, as<float>(g), 2 * I, ws) == hipSuccess &&
-         launch_swiglu_rows(s, as<float>(g), as<float>(a), I, T) == hipSuccess &&
+         launch_gemm_swiglu(s, as<float>(nrm), h, gu, I, h, T, as<float>(a), as<float>(g), ws) == hipSuccess &&
          launch_gemm(s, as<float>(a), I, down, h, I, T, as<float>(b), h, ws) == hipSuccess &&
          launch_residual_rows(s, as<float>(st), as<float>(b), as<uint16_t>(norms) + h, kMlpOffset, h, T) == hipSuccess &&
          hipMemcpyAsync(states, st.ptr, T * h * 4, hipMemcpyDeviceToHost, s) == hipSuccess &&

@@ -61,6 +61,7 @@ struct GemmWorkspace {
     uint32_t counters;
     uint16_t *planes;
     uint64_t plane_elems;
+    uint32_t cus;  // compute units (grid sizing)
 };
 struct GemmSplit {
     const float *x;
@@ -77,9 +78,11 @@ constexpr uint64_t kGemmPartialFloats = 16ull << 20;  // 64 MiB
 constexpr uint32_t kGemmCounters = 8192;
 // BF16 elements of the planes a GEMM of `tokens` rows and `cols` columns needs.
 uint64_t gemm_plane_elems(uint64_t tokens, uint64_t cols);
-// C[t, r] = sum_k X[t, k] * W[r, k]. With a workspace, more than one token
-// and K a multiple of 64: BF16 matrix cores on the exact three-term split of
-// X; otherwise FP32 MFMA with BF16 weights widened in LDS.
+// C[t, r] = sum_k X[t, k] * W[r, k]. With a workspace, at most 5 tokens and
+// K a multiple of 512: FP32 FMAs on the vector ALUs, weights streamed as in
+// the decode GEMV. Otherwise, with a workspace, more than one token and K a
+// multiple of 64: BF16 matrix cores on the exact three-term split of X; else
+// FP32 MFMA with BF16 weights widened in LDS.
 hipError_t launch_gemm(hipStream_t, const float *x, uint64_t x_stride, const uint16_t *w,
                        uint64_t rows, uint64_t cols, uint64_t tokens, float *y,
                        uint64_t y_stride, const GemmWorkspace *ws);
@@ -97,6 +100,13 @@ hipError_t launch_residual_rows(hipStream_t, float *state, const float *branch,
                                 const uint16_t *w, float offset, uint64_t width, uint64_t rows);
 hipError_t launch_swiglu_rows(hipStream_t, const float *gate_up, float *out,
                               uint64_t intermediate, uint64_t rows);
+// act[t, i] = silu(g) * u of the gate/up projection (rows i and
+// intermediate + i of w): the token GEMV writes act directly; other shapes
+// go through launch_gemm into gate_up ([tokens][2 * intermediate]) and
+// launch_swiglu_rows.
+hipError_t launch_gemm_swiglu(hipStream_t, const float *x, uint64_t x_stride, const uint16_t *w,
+                              uint64_t intermediate, uint64_t cols, uint64_t tokens, float *act,
+                              float *gate_up, const GemmWorkspace *ws);
 
 // Q/K head RMSNorm + RoPE + cache append for `tokens` rows of one layer.
 struct QkvPost {

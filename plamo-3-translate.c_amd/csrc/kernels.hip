@@ -79,6 +79,15 @@ __device__ __forceinline__ float rows_max(float v) {
                  fmaxf(lane_value(v, 32), lane_value(v, 48)));
 }
 __device__ __forceinline__ float wave_sum(float v) { return rows_sum(row_sum16(v)); }
+// wave_sum's value in lane 63 alone, without scalar registers: after the row
+// sums, row 1 adds row 0's and row 3 row 2's (row_bcast:15), then row 3 adds
+// lane 31's (row_bcast:31), so lane 63 holds (r2 + r3) + (r0 + r1).
+__device__ __forceinline__ float wave_total(float v) {
+    v = row_sum16(v);
+    v = v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x142, 0xA, 0xF, false));
+    v = v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x143, 0xC, 0xF, false));
+    return v;
+}
 __device__ __forceinline__ float wave_max(float v) { return rows_max(row_max16(v)); }
 
 // Cross-block hand-off without a device-scope fence (which writes back and
@@ -1524,6 +1533,316 @@ static bool skinny_supported(const float *x, uint64_t x_stride, const uint16_t *
            skinny_slices(cols, tokens, 1 << 20) != 0;
 }
 
+// ---------------------------------------------------------------- token GEMV
+// C[t, r] = sum_k X[t, k] * W[r, k] for 1..5 tokens (candidate verification,
+// short prompts) on the vector ALUs, with the decode GEMV's weight stream:
+// lane l reads the 16 bytes at column 512 c + 8 l of a row, so one load
+// instruction covers 1 KB of one row (the matrix-core operand layout covers
+// 16 rows x 64 B per instruction and streams about a third slower).
+//
+// Grid (row groups, K slices). A block stages X[:, slice] in LDS; each wave
+// takes units of U = 8 rows (with SwiGLU: gate rows 4j .. 4j + 3 and up rows
+// half + 4j .. half + 4j + 3) and streams a unit over the slice KC = 2 chunks
+// (16 KB) per sub-step, two sub-steps in flight. Each x read from LDS feeds
+// U rows: fewer rows per unit left the waves waiting on LDS. Every weight is multiplied
+// into T accumulators (per lane, row and token one FMA chain in column
+// order); the 64 lanes are summed once per unit (wave butterfly) and the sums
+// staged in LDS. With one slice they are the results; with several, each
+// block writes its sums through to the workspace and the last block of a row
+// group adds the slices in order, so results are run-to-run deterministic.
+struct TokenGemv {
+    const float *x;
+    uint64_t ldx;
+    const uint16_t *w;
+    uint32_t n, k, ks, slices, half, local;
+    float *y;
+    uint64_t ldy;
+    float *partial;
+    uint32_t *counters;
+};
+
+// Up to five tokens the vector ALUs keep pace with the weight stream; from
+// six, the x reads from LDS (2 T / U bytes per weight byte) bound the kernel
+// and the matrix-core skinny GEMM is faster.
+constexpr uint32_t kTokenMax = 5;
+constexpr uint32_t kTokenU = 8;
+constexpr uint32_t kTokenKC = 2;
+constexpr uint32_t kTokenXBytes = 64 * 1024;    // X slice per block
+constexpr uint32_t kTokenLdsBytes = 80 * 1024;  // X slice + staged sums: two blocks per CU
+
+template <int T>
+__global__ __launch_bounds__(256, 2) void token_gemv_kernel(TokenGemv g) {
+    constexpr uint32_t U = kTokenU, KC = kTokenKC, UT = U * T, H = U / 2;
+    extern __shared__ float tg_lds[];
+    // X slice [T][ks], each 512-column chunk as two planes: lane l's columns
+    // 8 l .. 8 l + 3 at 4 l, and 8 l + 4 .. 8 l + 7 at 256 + 4 l, so both of a
+    // lane's 16-byte reads are 1 KB contiguous across the wave.
+    float *xs = tg_lds;
+    float *outs = tg_lds + T * g.ks;  // [wave][local][U][T]
+    __shared__ int is_last;
+    const uint32_t lane = threadIdx.x & 63;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t k0 = blockIdx.y * g.ks;
+    const uint32_t chunks = g.ks / 512, nsub = (chunks + KC - 1) / KC;
+    const bool swiglu = g.half != 0;
+    const uint32_t units = swiglu ? g.half / H : (g.n + U - 1) / U;
+    const uint32_t first = blockIdx.x * 4 + wave, stride = gridDim.x * 4;
+    const uint32_t mine = first < units ? (units - first + stride - 1) / stride : 0;
+    const uint16_t *wl = g.w + k0 + lane * 8;
+    const uint32_t last = g.n - 1;
+
+    u32x4 a0[U][KC], a1[U][KC];
+    // One sub-step's loads. Past the wave's last unit, or past the slice's
+    // last chunk, every lane reads the matrix's first 16 bytes instead: the
+    // number of loads stays fixed, so the compiler's wait counts stay exact.
+    auto load = [&](u32x4 (&a)[U][KC], uint32_t ul, uint32_t sub) {
+        const bool v = ul < mine;
+        const uint32_t unit = first + ul * stride;
+#pragma unroll
+        for (uint32_t u = 0; u < U; ++u) {
+            uint32_t r = swiglu ? (u < H ? H * unit + u : g.half + H * unit + (u - H))
+                                : unit * U + u;
+            r = r > last ? last : r;
+            const uint16_t *p = wl + (uint64_t)r * g.k + sub * (KC * 512);
+#pragma unroll
+            for (uint32_t c = 0; c < KC; ++c) {
+                const bool ok = v && sub * KC + c < chunks;
+                a[u][c] = __builtin_nontemporal_load((const u32x4 *)(ok ? p + c * 512 : g.w));
+            }
+        }
+    };
+    float acc[U][T];
+#pragma unroll
+    for (uint32_t u = 0; u < U; ++u)
+#pragma unroll
+        for (int t = 0; t < T; ++t) acc[u][t] = 0.0f;
+    auto step = [&](const u32x4 (&a)[U][KC], uint32_t ul, uint32_t sub) {
+#pragma unroll
+        for (uint32_t c = 0; c < KC; ++c) {
+            const uint32_t chunk = sub * KC + c;
+            if (chunk < chunks) {
+                const float *xc = xs + chunk * 512 + lane * 4;
+                float xv[T][8];
+#pragma unroll
+                for (int t = 0; t < T; ++t) {
+                    const f32x4 p = *(const f32x4 *)(xc + t * g.ks);
+                    const f32x4 q = *(const f32x4 *)(xc + t * g.ks + 256);
+                    xv[t][0] = p.x; xv[t][1] = p.y; xv[t][2] = p.z; xv[t][3] = p.w;
+                    xv[t][4] = q.x; xv[t][5] = q.y; xv[t][6] = q.z; xv[t][7] = q.w;
+                }
+#pragma unroll
+                for (uint32_t u = 0; u < U; ++u) {
+                    const uint32_t q[4] = {a[u][c].x, a[u][c].y, a[u][c].z, a[u][c].w};
+                    float wv[8];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        wv[2 * e] = bf16f(q[e] & 0xffffu);
+                        wv[2 * e + 1] = __uint_as_float(q[e] & 0xffff0000u);
+                    }
+#pragma unroll
+                    for (int t = 0; t < T; ++t)
+#pragma unroll
+                        for (int e = 0; e < 8; ++e)
+                            acc[u][t] = __builtin_fmaf(wv[e], xv[t][e], acc[u][t]);
+                }
+            }
+        }
+        if (sub + 1 == nsub) {  // the unit's slice is done
+            float *o = outs + (wave * g.local + ul) * UT;
+#pragma unroll
+            for (uint32_t u = 0; u < U; ++u)
+#pragma unroll
+                for (int t = 0; t < T; ++t) {
+                    const float s = wave_total(acc[u][t]);
+                    if (lane == 63) o[u * T + t] = s;
+                    acc[u][t] = 0.0f;
+                }
+        }
+    };
+    auto advance = [&](uint32_t &ul, uint32_t &sub) {
+        if (++sub == nsub) {
+            sub = 0;
+            ++ul;
+        }
+    };
+
+    uint32_t lu = 0, ls = 0;  // next sub-step to load
+    // The prologue issues a0's loads strictly before a1's, as the loop does:
+    // the wait counts at the loop head merge both orders.
+    load(a0, lu, ls);
+    advance(lu, ls);
+    __builtin_amdgcn_sched_barrier(0);
+    load(a1, lu, ls);
+    advance(lu, ls);
+    __builtin_amdgcn_sched_barrier(0);
+    // Stage X[:, slice] (eight loads in flight per thread and trip). Indices
+    // past the end repeat the last element, loads and stores alike, so every
+    // load is consumed by a store and none is left pending into the loop
+    // (where its register would be waited for on every trip).
+    const uint32_t q4 = g.ks / 4, total = T * q4;
+    for (uint32_t e0 = threadIdx.x; e0 < total; e0 += 256 * 8) {
+        f32x4 v[8];
+        uint32_t at[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            at[j] = min(e0 + 256 * j, total - 1);
+            const uint32_t tok = at[j] / q4, c = (at[j] - tok * q4) * 4;
+            v[j] = *(const f32x4 *)(g.x + (uint64_t)tok * g.ldx + k0 + c);
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            // Column c (a multiple of 4) of a chunk: lane c / 8, plane c / 4 % 2.
+            const uint32_t f = at[j] * 4, c = f % 512;
+            *(f32x4 *)(xs + (f - c) + (c / 4 % 2) * 256 + c / 8 * 4) = v[j];
+        }
+    }
+    __syncthreads();
+    const uint32_t items = mine * nsub;
+    uint32_t cu = 0, cs = 0;  // next sub-step to compute
+    for (uint32_t i = 0; i < items; i += 2) {
+        step(a0, cu, cs);
+        advance(cu, cs);
+        __builtin_amdgcn_sched_barrier(0);
+        load(a0, lu, ls);
+        advance(lu, ls);
+        __builtin_amdgcn_sched_barrier(0);
+        if (i + 1 < items) {
+            step(a1, cu, cs);
+            advance(cu, cs);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        load(a1, lu, ls);
+        advance(lu, ls);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    __syncthreads();
+
+    const uint32_t per = 4 * g.local * UT;  // staged sums of the block
+    if (g.slices > 1) {
+        float *part = g.partial + ((uint64_t)blockIdx.y * gridDim.x + blockIdx.x) * per;
+        for (uint32_t e = threadIdx.x; e < per; e += 256) store_through(part + e, outs[e]);
+        if (!arrive_last(&g.counters[blockIdx.x], g.slices, &is_last)) return;
+        for (uint32_t e = threadIdx.x; e < per; e += 256) {
+            const float *p = g.partial + (uint64_t)blockIdx.x * per + e;
+            float s = load_through(p);
+            for (uint32_t sl = 1; sl < g.slices; ++sl)
+                s += load_through(p + (uint64_t)sl * gridDim.x * per);
+            outs[e] = s;
+        }
+        __syncthreads();
+    }
+    if (swiglu) {
+        // silu(gate) * up (tests/activation_reference.s:99-126).
+        for (uint32_t e = threadIdx.x; e < 4 * g.local * H * T; e += 256) {
+            const uint32_t t = e % T, u = (e / T) % H, wl_ = e / (H * T);  // wl_ = w * local + ul
+            const uint32_t w = wl_ / g.local, ul = wl_ - w * g.local;
+            const uint32_t unit = blockIdx.x * 4 + w + ul * stride;
+            if (unit >= units) continue;
+            const float gt = outs[(wl_ * U + u) * T + t], up = outs[(wl_ * U + u + H) * T + t];
+            const float d = plamo_exp(-gt) + 1.0f;
+            g.y[(uint64_t)t * g.ldy + H * unit + u] = (gt / d) * up;
+        }
+    } else {
+        for (uint32_t e = threadIdx.x; e < per; e += 256) {
+            const uint32_t t = e % T, u = (e / T) % U, wl_ = e / UT;
+            const uint32_t w = wl_ / g.local, ul = wl_ - w * g.local;
+            const uint32_t unit = blockIdx.x * 4 + w + ul * stride, row = unit * U + u;
+            if (unit < units && row < g.n) g.y[(uint64_t)t * g.ldy + row] = outs[e];
+        }
+    }
+}
+
+struct TokenPlan {
+    uint32_t slices, ks, blocks, local;
+    size_t lds;
+};
+
+// Slices: the fewest (dividing the 512-column chunks) whose X slice fits
+// kTokenXBytes. Row groups: two blocks per CU over all slices, fewer when
+// rows run out, more when the staged sums would not fit the LDS budget.
+static bool token_plan(uint64_t rows, uint64_t cols, uint64_t tokens, uint64_t half,
+                       uint32_t cus, TokenPlan &p) {
+    if (!tokens || tokens > kTokenMax || !rows || cols % 512 || cols > (1u << 30) ||
+        rows >= (1u << 30) || (half && (half % (kTokenU / 2) || rows != 2 * half)))
+        return false;
+    const uint64_t chunks = cols / 512;
+    uint64_t slices = 0;
+    for (uint64_t d = 1; d <= chunks && !slices; ++d)
+        if (chunks % d == 0 && tokens * (cols / d) * 4 <= kTokenXBytes) slices = d;
+    if (!slices) return false;
+    const uint64_t ks = cols / slices;
+    const uint64_t units = half ? half / (kTokenU / 2) : (rows + kTokenU - 1) / kTokenU;
+    uint64_t blocks = std::max<uint64_t>(1, 2ull * std::max<uint32_t>(cus, 1) / slices);
+    blocks = std::min<uint64_t>(blocks, (units + 3) / 4);
+    const uint64_t max_local = (kTokenLdsBytes / 4 / tokens - ks) / (4 * kTokenU);
+    uint64_t local = (units + 4 * blocks - 1) / (4 * blocks);
+    if (local > max_local) {
+        blocks = (units + 4 * max_local - 1) / (4 * max_local);
+        local = (units + 4 * blocks - 1) / (4 * blocks);
+    }
+    if (blocks > 65535) return false;
+    p.slices = (uint32_t)slices;
+    p.ks = (uint32_t)ks;
+    p.blocks = (uint32_t)blocks;
+    p.local = (uint32_t)local;
+    p.lds = (size_t)tokens * (ks + 4 * kTokenU * local) * 4;
+    return true;
+}
+
+template <int T>
+static hipError_t token_gemv_variant(hipStream_t stream, const TokenGemv &g, const TokenPlan &p) {
+    static bool wide = false;  // LDS above the default 64 KiB allowed once
+    if (p.lds > 65536 && !wide) {
+        hipError_t e = hipFuncSetAttribute((const void *)token_gemv_kernel<T>,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize,
+                                           (int)kTokenLdsBytes);
+        if (e != hipSuccess) return e;
+        wide = true;
+    }
+    token_gemv_kernel<T><<<dim3(p.blocks, p.slices), 256, p.lds, stream>>>(g);
+    return hipGetLastError();
+}
+
+// hipErrorNotSupported (nothing launched) when the shape or the workspace
+// does not fit the token GEMV.
+static hipError_t launch_token_gemv(hipStream_t stream, const float *x, uint64_t x_stride,
+                                    const uint16_t *w, uint64_t rows, uint64_t cols,
+                                    uint64_t tokens, uint64_t half, float *y, uint64_t y_stride,
+                                    const GemmWorkspace *ws) {
+    TokenPlan p;
+    if (!ws || !token_plan(rows, cols, tokens, half, ws->cus, p) || x_stride % 4 ||
+        ((uintptr_t)x & 15) || ((uintptr_t)w & 15))
+        return hipErrorNotSupported;
+    if (p.slices > 1 && (!ws->partial || !ws->counter_base || p.blocks > ws->counters ||
+                         (uint64_t)p.slices * p.blocks * 4 * p.local * kTokenU * tokens >
+                             ws->partial_floats))
+        return hipErrorNotSupported;
+    TokenGemv g{};
+    g.x = x;
+    g.ldx = x_stride;
+    g.w = w;
+    g.n = (uint32_t)rows;
+    g.k = (uint32_t)cols;
+    g.ks = p.ks;
+    g.slices = p.slices;
+    g.half = (uint32_t)half;
+    g.local = p.local;
+    g.y = y;
+    g.ldy = y_stride;
+    g.partial = ws->partial;
+    g.counters = ws->counter_base;
+    switch (tokens) {
+    case 1: return token_gemv_variant<1>(stream, g, p);
+    case 2: return token_gemv_variant<2>(stream, g, p);
+    case 3: return token_gemv_variant<3>(stream, g, p);
+    case 4: return token_gemv_variant<4>(stream, g, p);
+    case 5: return token_gemv_variant<5>(stream, g, p);
+    case 6: return token_gemv_variant<6>(stream, g, p);
+    case 7: return token_gemv_variant<7>(stream, g, p);
+    default: return token_gemv_variant<8>(stream, g, p);
+    }
+}
+
 static bool gemm_split_supported(const float *x, uint64_t x_stride, const uint16_t *w,
                                  uint64_t cols) {
     return cols % (2 * kSplitBK) == 0 && x_stride % 4 == 0 && !((uintptr_t)x & 15) &&
@@ -1538,6 +1857,11 @@ hipError_t launch_gemm(hipStream_t stream, const float *x, uint64_t x_stride, co
                        uint64_t rows, uint64_t cols, uint64_t tokens, float *y,
                        uint64_t y_stride, const GemmWorkspace *ws) {
     if (!tokens || !rows) return hipSuccess;
+    {
+        hipError_t e = launch_token_gemv(stream, x, x_stride, w, rows, cols, tokens, 0, y,
+                                         y_stride, ws);
+        if (e != hipErrorNotSupported) return e;
+    }
     if (skinny_supported(x, x_stride, w, rows, cols, tokens)) {
         SkinnyGemm g{};
         g.x = x;
@@ -1575,6 +1899,20 @@ hipError_t launch_gemm(hipStream_t stream, const float *x, uint64_t x_stride, co
     }
     if (tokens <= 16) return gemm_variant<16, 64>(stream, x, x_stride, w, rows, cols, tokens, y, y_stride);
     return gemm_variant<64, 64>(stream, x, x_stride, w, rows, cols, tokens, y, y_stride);
+}
+
+hipError_t launch_gemm_swiglu(hipStream_t stream, const float *x, uint64_t x_stride,
+                              const uint16_t *w, uint64_t intermediate, uint64_t cols,
+                              uint64_t tokens, float *act, float *gate_up,
+                              const GemmWorkspace *ws) {
+    if (!tokens || !intermediate) return hipSuccess;
+    hipError_t e = launch_token_gemv(stream, x, x_stride, w, 2 * intermediate, cols, tokens,
+                                     intermediate, act, intermediate, ws);
+    if (e != hipErrorNotSupported) return e;
+    e = launch_gemm(stream, x, x_stride, w, 2 * intermediate, cols, tokens, gate_up,
+                    2 * intermediate, ws);
+    if (e != hipSuccess) return e;
+    return launch_swiglu_rows(stream, gate_up, act, intermediate, tokens);
 }
 
 // ---------------------------------------------------------------- row norms
