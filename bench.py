@@ -141,6 +141,56 @@ def measured_traffic():
     return None
 
 
+def verify_sweep(args) -> dict:
+    """The target's batched candidate verification alone (plamo_metal_verify,
+    runtime/metal_model.m:829-830 semantics) on the C5 model (tied head) after
+    a 455-token prompt: the median time of one verify of T candidates for
+    each T in --verify-tokens, beside the decode step of the same model. One
+    to five candidates stream the projections through the token GEMV, more
+    through the matrix-core skinny GEMM."""
+    tcfg = dict(plamo_hip.CONFIGS["c5"])
+    tied = tcfg.pop("tied", 0)
+    threads = min(16, os.cpu_count() or 1)
+    target = plamo_hip.Synthetic(**tcfg, tied=tied, seed=20261201, threads=threads)
+    inst = target.instance(pinned=True)
+    be = plamo_hip.Backend(target)
+    rng = np.random.default_rng(11)
+    prompt = rng.integers(0, tcfg["vocab"], size=455).astype(np.uint32).tolist()
+    if be.prefill(inst, prompt) != 1:
+        raise RuntimeError(be.info().note.decode())
+    verify_ms = {}
+    for n in [int(x) for x in args.verify_tokens.split(",") if x]:
+        times = []
+        for _ in range(5):
+            start = time.perf_counter()
+            ok, _ = be.verify(inst, prompt[:n])
+            times.append((time.perf_counter() - start) * 1e3)
+            if ok != 1:
+                raise RuntimeError(be.info().note.decode())
+        verify_ms[str(n)] = round(float(np.median(times[1:])), 3)
+        log(f"verify({n}) {verify_ms[str(n)]:.3f} ms (runs {[round(t, 2) for t in times]})")
+    token = int(np.argmax(inst.logits()))
+    steps = []
+    for _ in range(6):
+        start = time.perf_counter()
+        if be.forward(inst, token) != 1:
+            raise RuntimeError(be.info().note.decode())
+        steps.append((time.perf_counter() - start) * 1e3)
+        token = int(np.argmax(inst.logits()))
+    info = be.info()
+    assert info.errors == 0 and info.cpu_fallbacks == 0, info.note.decode()
+    be.close()
+    inst.close()
+    target.close()
+    return {"metric": "batched verify latency (31B-class target)", "unit": "ms",
+            "higher_is_better": False, "n_gpus": 1, "dtype": "fp32",
+            "data": "synthetic (seeded BF16 weights ~N(0,0.02); uniform random prompt ids)",
+            "config": {"workload": "c5 target (tied head), 455-token prompt, one verify of "
+                                   "T candidates per call"},
+            "verify_ms": verify_ms,
+            "decode_step_ms": round(float(np.median(steps[1:])), 3)}
+
+
 def speculative(args) -> dict:
     """the 31B-class model (C5, tied embedding/head) with
     the 0.8B-class model (C2 shape) as the in-process draft, 4 draft tokens
@@ -267,6 +317,9 @@ def main() -> int:
                          "kernel that scales rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     ap.add_argument("--speculative", action="store_true",
                     help="measure BASELINE configs[4] (C5 target, 0.8B-class draft) instead")
+    ap.add_argument("--verify", action="store_true",
+                    help="time the C5 target's batched verify alone, per candidate count")
+    ap.add_argument("--verify-tokens", default="1,2,3,4,5,6,8,16")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path "
@@ -275,6 +328,9 @@ def main() -> int:
         return 2
     if args.speculative:
         print(json.dumps(speculative(args)), flush=True)
+        return 0
+    if args.verify:
+        print(json.dumps(verify_sweep(args)), flush=True)
         return 0
     cfg = dict(plamo_hip.CONFIGS[args.config])
     cfg["name"] = args.config
