@@ -3037,8 +3037,9 @@ __global__ __launch_bounds__(128) void attention_merge_kernel(const float *parti
     }
 }
 
-// Key splits: only when the query tiles alone leave the GPU mostly idle;
-// splits of at least two key tiles, at most 64, within the scratch bound.
+// Key splits: only when the query tiles alone leave the GPU mostly idle (a
+// few candidate or prompt tokens over a long prefix): about four blocks per
+// CU of one key tile each, at most 64 splits, within the scratch bound.
 constexpr uint64_t kAttentionScratchFloats = 8ull << 20;
 static uint32_t prompt_attention_splits(uint32_t prefix, uint32_t tokens, uint32_t qh,
                                         uint32_t dim, uint32_t *split_rows) {
@@ -3046,8 +3047,8 @@ static uint32_t prompt_attention_splits(uint32_t prefix, uint32_t tokens, uint32
     const uint32_t blocks = qh * tiles;
     *split_rows = 0;
     if (blocks >= 256 || keys <= 2 * kKT) return 1;
-    uint32_t splits = (512 + blocks - 1) / blocks;
-    splits = min(splits, min(64u, (keys + 2 * kKT - 1) / (2 * kKT)));
+    uint32_t splits = (1024 + blocks - 1) / blocks;
+    splits = min(splits, min(64u, (keys + kKT - 1) / kKT));
     while (splits > 1 && (uint64_t)splits * tokens * qh * (dim + 2) > kAttentionScratchFloats)
         --splits;
     if (splits <= 1) return 1;
