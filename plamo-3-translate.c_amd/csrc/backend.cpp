@@ -1637,7 +1637,7 @@ int plamo_metal_linear(struct plamo_metal *m, const struct plamo_matmul *mm) {
     uint64_t T = mm->tokens, K = mm->columns, N = mm->rows;
     Buffer &in = m->lin_in, &out = m->lin_out;
     if (!ensure(m, in, T * K * 4) || !ensure(m, out, T * N * 4)) return 0;
-    if (T == 1 && configure_gemv(K) != hipSuccess) {
+    if (configure_gemv(K) != hipSuccess) {
         (void)hipGetLastError();
         return 0;
     }

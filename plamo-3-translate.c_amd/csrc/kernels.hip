@@ -857,7 +857,11 @@ static bool gemv_reg_launch(hipStream_t stream, const uint16_t *w, uint64_t rows
     }
 }
 
+static hipError_t configure_token_gemv();
+
 hipError_t configure_gemv(uint64_t max_cols) {
+    hipError_t e = configure_token_gemv();
+    if (e != hipSuccess) return e;
     int lds = (int)(max_cols * sizeof(float));
     if (lds <= 65536) return hipSuccess;
     const void *kernels[] = {(const void *)gemv_kernel<true, true>, (const void *)gemv_kernel<true, false>,
@@ -1572,6 +1576,7 @@ constexpr uint32_t kTokenLdsBytes = 80 * 1024;  // X slice + staged sums: two bl
 
 template <int T>
 __global__ __launch_bounds__(256, 2) void token_gemv_kernel(TokenGemv g) {
+    static_assert(T >= 1 && T <= (int)kTokenMax, "token count the plan admits");
     constexpr uint32_t U = kTokenU, KC = kTokenKC, UT = U * T, H = U / 2;
     extern __shared__ float tg_lds[];
     // X slice [T][ks], each 512-column chunk as two planes: lane l's columns
@@ -1789,16 +1794,21 @@ static bool token_plan(uint64_t rows, uint64_t cols, uint64_t tokens, uint64_t h
     return true;
 }
 
-template <int T>
-static hipError_t token_gemv_variant(hipStream_t stream, const TokenGemv &g, const TokenPlan &p) {
-    static bool wide = false;  // LDS above the default 64 KiB allowed once
-    if (p.lds > 65536 && !wide) {
-        hipError_t e = hipFuncSetAttribute((const void *)token_gemv_kernel<T>,
-                                           hipFuncAttributeMaxDynamicSharedMemorySize,
+// The token GEMV stages up to kTokenLdsBytes, above the default 64 KiB.
+static hipError_t configure_token_gemv() {
+    const void *kernels[] = {(const void *)token_gemv_kernel<1>, (const void *)token_gemv_kernel<2>,
+                             (const void *)token_gemv_kernel<3>, (const void *)token_gemv_kernel<4>,
+                             (const void *)token_gemv_kernel<5>};
+    for (const void *k : kernels) {
+        hipError_t e = hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize,
                                            (int)kTokenLdsBytes);
         if (e != hipSuccess) return e;
-        wide = true;
     }
+    return hipSuccess;
+}
+
+template <int T>
+static hipError_t token_gemv_variant(hipStream_t stream, const TokenGemv &g, const TokenPlan &p) {
     token_gemv_kernel<T><<<dim3(p.blocks, p.slices), 256, p.lds, stream>>>(g);
     return hipGetLastError();
 }
@@ -1836,10 +1846,7 @@ static hipError_t launch_token_gemv(hipStream_t stream, const float *x, uint64_t
     case 2: return token_gemv_variant<2>(stream, g, p);
     case 3: return token_gemv_variant<3>(stream, g, p);
     case 4: return token_gemv_variant<4>(stream, g, p);
-    case 5: return token_gemv_variant<5>(stream, g, p);
-    case 6: return token_gemv_variant<6>(stream, g, p);
-    case 7: return token_gemv_variant<7>(stream, g, p);
-    default: return token_gemv_variant<8>(stream, g, p);
+    default: return token_gemv_variant<5>(stream, g, p);
     }
 }
 
