@@ -114,7 +114,8 @@ static struct {
     const float *x;
     float *y;
     uint64_t rows, cols;
-} pool = {PTHREAD_MUTEX_INITIALIZER, PTHREAD_COND_INITIALIZER, PTHREAD_COND_INITIALIZER};
+} pool = {.mutex = PTHREAD_MUTEX_INITIALIZER, .start = PTHREAD_COND_INITIALIZER,
+          .done = PTHREAD_COND_INITIALIZER};
 
 static void pool_slice(unsigned index) {
     uint64_t groups = (pool.rows + ROW_GROUP - 1) / ROW_GROUP;

@@ -1,8 +1,8 @@
 /* CPU oracle of the PLaMo-3-Translate token loop — TEST INFRASTRUCTURE ONLY.
  *
  * A scalar C restatement of the reference's FP32 CPU path, in the exact
- * operation order of its bit-exact specification (tests/*_reference.s) and
- * of the production assembly that is bit-identical to it (src/*.s). It is the
+ * operation order of its bit-exact specification (the tests/..._reference.s files) and
+ * of the production assembly that is bit-identical to it (the src/ assembly). It is the
  * checker for the HIP backend and the CPU baseline of bench.py; nothing in the
  * product links or calls it. Every function names the reference file:line it
  * follows in plamo_oracle.c.
