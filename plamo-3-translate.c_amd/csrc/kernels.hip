@@ -1779,7 +1779,10 @@ static bool token_plan(uint64_t rows, uint64_t cols, uint64_t tokens, uint64_t h
     const uint64_t units = half ? half / (kTokenU / 2) : (rows + kTokenU - 1) / kTokenU;
     uint64_t blocks = std::max<uint64_t>(1, 2ull * std::max<uint32_t>(cus, 1) / slices);
     blocks = std::min<uint64_t>(blocks, (units + 3) / 4);
-    const uint64_t max_local = (kTokenLdsBytes / 4 / tokens - ks) / (4 * kTokenU);
+    const uint64_t budget = kTokenLdsBytes / 4 / tokens;  // floats per block per token
+    if (budget <= ks) return false;
+    const uint64_t max_local = (budget - ks) / (4 * kTokenU);
+    if (!max_local) return false;
     uint64_t local = (units + 4 * blocks - 1) / (4 * blocks);
     if (local > max_local) {
         blocks = (units + 4 * max_local - 1) / (4 * max_local);
