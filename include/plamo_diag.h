@@ -30,6 +30,14 @@ enum plamo_hip_kernel {
 int plamo_hip_time_kernel(struct plamo_metal *, struct model *, uint64_t layer, int which,
                           int reps, double *ms_per_launch, double *bytes_per_launch);
 
+/* Test hook of the failure contract (runtime/metal.h:63-67): from the next
+ * call on, the decode attention's output-projection blocks wait for `extra`
+ * more finished KV heads than exist and give up after `polls` polls
+ * (0: the default bound), so the call must return -1 with one counted error
+ * while every kernel still exits normally. plamo_hip_debug_waits(m, 0, 0)
+ * restores the normal waits. No counterpart in the reference. */
+void plamo_hip_debug_waits(struct plamo_metal *, uint32_t extra, uint32_t polls);
+
 #ifdef __cplusplus
 }
 #endif

@@ -7,6 +7,7 @@
  */
 #define _GNU_SOURCE
 #include "plamo_oracle.h"
+#include <immintrin.h>
 #include <math.h>
 #include <pthread.h>
 #include <stdlib.h>
@@ -100,20 +101,124 @@ static void matvec_rows(const uint16_t *w, const float *x, float *y, uint64_t ro
     }
 }
 
+/* The same products for a block of tokens (src/matmul.s:1-4: a matmul is,
+ * bit for bit, one matvec per token). Each weight row is widened once per
+ * block of TOKEN_BLOCK tokens; the block's inputs are interleaved in pairs of
+ * tokens ([x_a(k..k+3) | x_b(k..k+3)] for every k step of 4), so one 8-wide
+ * fused multiply-add serves two tokens. Per token the arithmetic is
+ * matvec_rows' own: lane l accumulates k = l mod 4, then (a0 + a1) +
+ * (a2 + a3), then the sequential tail; the tokens only share the weight loads. */
+enum { TOKEN_BLOCK = 64 };
+
+static __thread float *widened, *pairs;
+static __thread uint64_t widened_cols;
+
+/* BF16 -> FP32 of a row, eight at a time (the 16-bit shift of oracle_bf16). */
+static void widen_row(const uint16_t *src, float *dst, uint64_t cols) {
+    uint64_t k = 0;
+    for (; k + 8 <= cols; k += 8) {
+        __m256i v = _mm256_cvtepu16_epi32(_mm_loadu_si128((const __m128i *)(src + k)));
+        _mm256_storeu_si256((__m256i *)(dst + k), _mm256_slli_epi32(v, 16));
+    }
+    for (; k < cols; ++k)
+        dst[k] = oracle_bf16(src[k]);
+}
+
+static void lanes_to_sums(__m256 acc, const float *w, const float *xa, const float *xb,
+                          uint64_t cols, float *ya, float *yb) {
+    uint64_t body = cols / 4 * 4;
+    float l[8];
+    _mm256_storeu_ps(l, acc);
+    float sa = (l[0] + l[1]) + (l[2] + l[3]), sb = (l[4] + l[5]) + (l[6] + l[7]);
+    for (uint64_t k = body; k < cols; ++k) {
+        sa = fmaf(w[k], xa[k], sa);
+        sb = fmaf(w[k], xb[k], sb);
+    }
+    *ya = sa;
+    if (yb)
+        *yb = sb;
+}
+
+static void matmul_rows(const uint16_t *w, const float *x, uint64_t x_stride, float *y,
+                        uint64_t y_stride, uint64_t rows, uint64_t cols, uint64_t tokens) {
+    enum { RB = 4 };  /* weight rows per register block (times two token pairs) */
+    const uint64_t body = cols / 4 * 4;
+    if (widened_cols < cols) {
+        free(widened);
+        free(pairs);
+        widened = malloc(RB * cols * sizeof(float));
+        pairs = malloc((uint64_t)TOKEN_BLOCK * (body + 4) * sizeof(float));
+        widened_cols = widened && pairs ? cols : 0;
+        if (!widened_cols)
+            abort();
+    }
+    for (uint64_t t0 = 0; t0 < tokens; t0 += TOKEN_BLOCK) {
+        const uint64_t t1 = t0 + TOKEN_BLOCK < tokens ? t0 + TOKEN_BLOCK : tokens;
+        const uint64_t np = (t1 - t0 + 1) / 2;  /* token pairs (the last may be single) */
+        for (uint64_t p = 0; p < np; ++p) {
+            const float *xa = x + (t0 + 2 * p) * x_stride;
+            const float *xb = t0 + 2 * p + 1 < t1 ? xa + x_stride : xa;
+            float *dst = pairs + p * 2 * body;
+            for (uint64_t k = 0; k < body; k += 4) {
+                memcpy(dst + 2 * k, xa + k, 16);
+                memcpy(dst + 2 * k + 4, xb + k, 16);
+            }
+        }
+        for (uint64_t r0 = 0; r0 < rows; r0 += RB) {
+            const uint64_t nr = rows - r0 < RB ? rows - r0 : RB;
+            for (uint64_t i = 0; i < RB; ++i)
+                widen_row(w + (r0 + (i < nr ? i : 0)) * cols, widened + i * cols, cols);
+            const float *w0 = widened, *w1 = w0 + cols, *w2 = w1 + cols, *w3 = w2 + cols;
+            for (uint64_t p = 0; p < np; p += 2) {
+                const uint64_t q = np - p < 2 ? np - p : 2;
+                const float *x0 = pairs + p * 2 * body, *x1 = pairs + (p + q - 1) * 2 * body;
+                __m256 a00 = _mm256_setzero_ps(), a01 = a00, a10 = a00, a11 = a00, a20 = a00,
+                       a21 = a00, a30 = a00, a31 = a00;
+                for (uint64_t k = 0; k < body; k += 4) {
+                    const __m256 v0 = _mm256_loadu_ps(x0 + 2 * k), v1 = _mm256_loadu_ps(x1 + 2 * k);
+                    __m256 b = _mm256_broadcast_ps((const __m128 *)(w0 + k));
+                    a00 = _mm256_fmadd_ps(b, v0, a00);
+                    a01 = _mm256_fmadd_ps(b, v1, a01);
+                    b = _mm256_broadcast_ps((const __m128 *)(w1 + k));
+                    a10 = _mm256_fmadd_ps(b, v0, a10);
+                    a11 = _mm256_fmadd_ps(b, v1, a11);
+                    b = _mm256_broadcast_ps((const __m128 *)(w2 + k));
+                    a20 = _mm256_fmadd_ps(b, v0, a20);
+                    a21 = _mm256_fmadd_ps(b, v1, a21);
+                    b = _mm256_broadcast_ps((const __m128 *)(w3 + k));
+                    a30 = _mm256_fmadd_ps(b, v0, a30);
+                    a31 = _mm256_fmadd_ps(b, v1, a31);
+                }
+                const __m256 acc[RB][2] = {{a00, a01}, {a10, a11}, {a20, a21}, {a30, a31}};
+                for (uint64_t i = 0; i < nr; ++i)
+                    for (uint64_t j = 0; j < q; ++j) {
+                        const uint64_t ta = t0 + 2 * (p + j), tb = ta + 1;
+                        const float *xa = x + ta * x_stride;
+                        const int two = tb < t1;
+                        lanes_to_sums(acc[i][j], widened + i * cols, xa,
+                                      two ? xa + x_stride : xa, cols, y + ta * y_stride + r0 + i,
+                                      two ? y + tb * y_stride + r0 + i : NULL);
+                    }
+            }
+        }
+    }
+}
+
 /* Row-split thread pool for the CPU baseline: rows are cut in groups of 24
  * and handed out in contiguous slices, as runtime/parallel.c:35-48 does.
- * Splitting rows does not change any row's arithmetic. */
+ * Splitting rows does not change any row's arithmetic. A job is one matvec
+ * (tokens == 1) or the token-blocked products of a prompt. */
 enum { ROW_GROUP = 24, MAX_THREADS = 64 };
 static struct {
     pthread_mutex_t mutex;
     pthread_cond_t start, done;
     pthread_t threads[MAX_THREADS];
-    unsigned count, pending;
+    unsigned count, created, pending;  /* active threads, worker threads made + 1 */
     uint64_t generation;
     const uint16_t *w;
     const float *x;
     float *y;
-    uint64_t rows, cols;
+    uint64_t rows, cols, tokens, x_stride, y_stride;
 } pool = {.mutex = PTHREAD_MUTEX_INITIALIZER, .start = PTHREAD_COND_INITIALIZER,
           .done = PTHREAD_COND_INITIALIZER};
 
@@ -123,8 +228,13 @@ static void pool_slice(unsigned index) {
     uint64_t end = groups * (index + 1) / pool.count * ROW_GROUP;
     if (end > pool.rows)
         end = pool.rows;
-    if (first < end)
+    if (first >= end)
+        return;
+    if (pool.tokens == 1)
         matvec_rows(pool.w + first * pool.cols, pool.x, pool.y + first, end - first, pool.cols);
+    else
+        matmul_rows(pool.w + first * pool.cols, pool.x, pool.x_stride, pool.y + first,
+                    pool.y_stride, end - first, pool.cols, pool.tokens);
 }
 
 static void *pool_main(void *arg) {
@@ -135,6 +245,8 @@ static void *pool_main(void *arg) {
         while (seen == pool.generation)
             pthread_cond_wait(&pool.start, &pool.mutex);
         seen = pool.generation;
+        if (index >= pool.count)
+            continue; /* idle at the current thread count */
         pthread_mutex_unlock(&pool.mutex);
         pool_slice(index);
         pthread_mutex_lock(&pool.mutex);
@@ -150,11 +262,13 @@ void oracle_set_threads(unsigned threads) {
     if (threads > MAX_THREADS)
         threads = MAX_THREADS;
     pthread_mutex_lock(&pool.mutex);
-    /* Workers are only ever added; index 0 is the calling thread. */
-    for (unsigned i = pool.count ? pool.count : 1; i < threads; ++i)
+    /* Index 0 is the calling thread. Workers are made once and stay; those at
+     * or past the active count sit out each job. */
+    for (unsigned i = pool.created ? pool.created : 1; i < threads; ++i)
         pthread_create(&pool.threads[i], NULL, pool_main, (void *)(uintptr_t)i);
-    if (threads > pool.count)
-        pool.count = threads;
+    if (threads > pool.created)
+        pool.created = threads;
+    pool.count = threads;
     pthread_mutex_unlock(&pool.mutex);
 }
 
@@ -162,10 +276,14 @@ unsigned oracle_threads(void) {
     return pool.count ? pool.count : 1;
 }
 
-void oracle_matvec(const uint16_t *w, const float *x, float *y, uint64_t rows, uint64_t cols) {
+static void run_pool(const uint16_t *w, const float *x, uint64_t x_stride, float *y,
+                     uint64_t y_stride, uint64_t rows, uint64_t cols, uint64_t tokens) {
     unsigned threads = oracle_threads();
     if (threads <= 1 || rows < (uint64_t)threads * ROW_GROUP || rows * cols < 256 * 1024) {
-        matvec_rows(w, x, y, rows, cols);
+        if (tokens == 1)
+            matvec_rows(w, x, y, rows, cols);
+        else
+            matmul_rows(w, x, x_stride, y, y_stride, rows, cols, tokens);
         return;
     }
     pthread_mutex_lock(&pool.mutex);
@@ -174,6 +292,9 @@ void oracle_matvec(const uint16_t *w, const float *x, float *y, uint64_t rows, u
     pool.y = y;
     pool.rows = rows;
     pool.cols = cols;
+    pool.tokens = tokens;
+    pool.x_stride = x_stride;
+    pool.y_stride = y_stride;
     pool.pending = threads - 1;
     ++pool.generation;
     pthread_cond_broadcast(&pool.start);
@@ -185,11 +306,29 @@ void oracle_matvec(const uint16_t *w, const float *x, float *y, uint64_t rows, u
     pthread_mutex_unlock(&pool.mutex);
 }
 
+void oracle_matvec(const uint16_t *w, const float *x, float *y, uint64_t rows, uint64_t cols) {
+    run_pool(w, x, 0, y, 0, rows, cols, 1);
+}
+
 /* src/matmul.s:1-4: a matmul is, bit for bit, one matvec per token. */
 void oracle_matmul(const struct plamo_matmul *m) {
     for (uint64_t t = 0; t < m->tokens; ++t)
         oracle_matvec(m->weights, m->input + t * m->input_stride, m->output + t * m->output_stride,
                       m->rows, m->columns);
+}
+
+/* The token-blocked form of oracle_matmul (the same bits; the prefill's
+ * projections use it, as the reference's prompt path runs GEMM tiles,
+ * src/matmul8x3.s). */
+void oracle_matmul_blocked(const struct plamo_matmul *m) {
+    if (!m->tokens)
+        return;
+    if (m->tokens == 1) {
+        oracle_matvec(m->weights, m->input, m->output, m->rows, m->columns);
+        return;
+    }
+    run_pool(m->weights, m->input, m->input_stride, m->output, m->output_stride, m->rows,
+             m->columns, m->tokens);
 }
 
 /* tests/rmsnorm_reference.s:8-34. */
@@ -488,6 +627,57 @@ int oracle_forward_hidden(struct model *m, uint64_t token) {
     return forward_common(m, token, 0);
 }
 
+static void project(const uint16_t *w, const float *x, uint64_t x_stride, float *y,
+                    uint64_t y_stride, uint64_t rows, uint64_t cols, uint64_t tokens) {
+    struct plamo_matmul mm = {w, x, y, rows, cols, tokens, x_stride, y_stride};
+    oracle_matmul_blocked(&mm);
+}
+
+/* Workspace of one prompt: per token the normalized input, projection
+ * outputs, attention output, residual branch and SwiGLU activation. */
+struct prompt_rows {
+    float *norm, *qkv, *attn, *branch, *gu, *act;
+};
+
+/* src/batch.s:61-223 (_plamo_layer_batch): one layer over every prompt
+ * token. The projections run as token-blocked products (bit for bit one
+ * matvec per token); the Q/K norm, cache append, key rotation and attention
+ * run token by token in prompt order, since each token attends over the rows
+ * the earlier ones appended. Per token the operations are oracle_layer's. */
+static int layer_batch(struct layer *l, float scale, float *states, uint64_t n,
+                       const struct prompt_rows *b) {
+    struct mixer *mx = l->mixer;
+    const struct qkv *q = mx->qkv;
+    const struct mlp *p = l->mlp;
+    const uint64_t h = l->hidden, qw = (q->qh + 2 * q->kh) * q->dim;
+    const uint64_t aw = mx->gqa->qh * mx->gqa->dim, inter = p->intermediate;
+    for (uint64_t t = 0; t < n; ++t)
+        oracle_rmsnorm(states + t * h, l->pre, b->norm + t * h, h, 0.000001f, 1.0f);
+    project(q->weight, b->norm, h, b->qkv, qw, qw, h, n);
+    for (uint64_t t = 0; t < n; ++t) {
+        oracle_qk_norm(b->qkv + t * qw, q->qn, q->kn, q->qh, q->kh, q->dim);
+        if (!oracle_mixer_attention(mx, b->qkv + t * qw, b->attn + t * aw, scale))
+            return 0;
+    }
+    project(mx->weight, b->attn, aw, b->branch, h, h, aw, n);
+    for (uint64_t t = 0; t < n; ++t) {
+        float *br = b->branch + t * h, *st = states + t * h;
+        oracle_rmsnorm(br, l->post, br, h, 0.000001f, 0.2f);
+        oracle_residual(st, br, h);
+        oracle_rmsnorm(st, p->pre, b->norm + t * h, h, 0.000001f, 1.0f);
+    }
+    project(p->gu, b->norm, h, b->gu, 2 * inter, 2 * inter, h, n);
+    for (uint64_t t = 0; t < n; ++t)
+        oracle_swiglu(b->gu + t * 2 * inter, b->act + t * inter, inter);
+    project(p->down, b->act, inter, b->branch, h, h, inter, n);
+    for (uint64_t t = 0; t < n; ++t) {
+        float *br = b->branch + t * h;
+        oracle_rmsnorm(br, p->post, br, h, 0.000001f, 0.08944271909999159f);
+        oracle_residual(states + t * h, br, h);
+    }
+    return 1;
+}
+
 /* tests/prefill_reference.s:7-88: embeddings first, then layer-major over all
  * tokens; the final token's state, final norm and head give the logits. The
  * per-layer state pointer is restored to model->state afterwards, as the
@@ -495,28 +685,37 @@ int oracle_forward_hidden(struct model *m, uint64_t token) {
 int oracle_prefill(struct model *m, const uint32_t *ids, uint64_t n, float *states) {
     if (!n)
         return 0;
-    uint64_t h = m->hidden;
-    float *owned = NULL;
-    if (!states) {
-        owned = malloc(n * h * 4);
-        if (!owned)
-            return 0;
-        states = owned;
+    uint64_t h = m->hidden, qw = 0, aw = 0, inter = 0;
+    for (uint64_t i = 0; i < m->count; ++i) {
+        const struct mixer *mx = m->layers[i]->mixer;
+        uint64_t w = (mx->qkv->qh + 2 * mx->qkv->kh) * mx->qkv->dim;
+        qw = w > qw ? w : qw;
+        w = mx->gqa->qh * mx->gqa->dim;
+        aw = w > aw ? w : aw;
+        inter = m->layers[i]->mlp->intermediate > inter ? m->layers[i]->mlp->intermediate : inter;
     }
-    int ok = 1;
+    float *owned = states ? NULL : malloc(n * h * 4);
+    struct prompt_rows b = {malloc(n * h * 4), malloc(n * qw * 4), malloc(n * aw * 4),
+                            malloc(n * h * 4), malloc(n * 2 * inter * 4), malloc(n * inter * 4)};
+    if (!states)
+        states = owned;
+    int ok = states && b.norm && b.qkv && b.attn && b.branch && b.gu && b.act;
     for (uint64_t t = 0; t < n && ok; ++t)
         ok = oracle_embedding(m->embedding, ids[t], m->vocab, h, states + t * h);
     for (uint64_t i = 0; i < m->count && ok; ++i)
-        for (uint64_t t = 0; t < n && ok; ++t) {
-            m->layers[i]->state = states + t * h;
-            ok = oracle_layer(m->layers[i], m->scales[i]);
-        }
+        ok = layer_batch(m->layers[i], m->scales[i], states, n, &b);
     for (uint64_t i = 0; i < m->count; ++i)
         m->layers[i]->state = m->state;
     if (ok) {
         memcpy(m->state, states + (n - 1) * h, h * 4);
         final_head(m);
     }
+    free(b.norm);
+    free(b.qkv);
+    free(b.attn);
+    free(b.branch);
+    free(b.gu);
+    free(b.act);
     free(owned);
     return ok;
 }

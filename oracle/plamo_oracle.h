@@ -25,6 +25,7 @@ void oracle_softmax(float *x, uint64_t n);
 void oracle_swiglu(const float *gate_up, float *out, uint64_t n);
 void oracle_matvec(const uint16_t *w, const float *x, float *y, uint64_t rows, uint64_t cols);
 void oracle_matmul(const struct plamo_matmul *m);
+void oracle_matmul_blocked(const struct plamo_matmul *m);
 void oracle_set_threads(unsigned threads);
 unsigned oracle_threads(void);
 void oracle_rmsnorm(const float *x, const uint16_t *w, float *y, uint64_t n, float eps,

@@ -70,10 +70,11 @@ struct Layer {
     float *k = nullptr, *v = nullptr, *rot = nullptr;
     float *host_k = nullptr, *host_v = nullptr, *host_rot = nullptr;  // device views of pinned host rows
     uint64_t rows = 0;          // device rows allocated
-    // Shadow of the host bookkeeping after this backend's last return.
+    // Shadow of the host bookkeeping after this backend's last return: the
+    // counters and the last K and V rows ([K row | V row]).
     bool synced = false;
     uint64_t count = 0, processed = 0, scale_bits = 0;
-    std::vector<float> last_k;
+    std::vector<float> last_kv;
     uint64_t verify_prefix = 0;
     bool verify_stale = false;  // device rebuilt rotated rows the host still has stale
 };
@@ -96,6 +97,10 @@ struct plamo_metal {
     bool hooks = false;
 
     struct model *model = nullptr;
+    // What the prepared state was built from besides the descriptor address:
+    // host arrays, weights and shapes (a new model at a freed one's address
+    // must not inherit its graph or pinned-host views).
+    std::vector<uintptr_t> fingerprint;
     std::vector<Layer> layers;
     std::vector<RopeTable> ropes;
     const uint16_t *embedding = nullptr, *head = nullptr;
@@ -109,18 +114,15 @@ struct plamo_metal {
     float *state_a = nullptr, *state_b = nullptr, *qkv = nullptr, *q = nullptr, *attn = nullptr,
           *branch = nullptr, *act = nullptr, *down_out = nullptr, *partial = nullptr;
     uint32_t *counters = nullptr;
-    uint32_t *layer_counters = nullptr;  // one-launch layers: kLayerCounterWords per layer
     float *outbox = nullptr, *outbox_host = nullptr;  // logits | state | normalized | stage
     uint64_t outbox_floats = 0;
     // When every host array a step updates is pinned and device-visible, the
     // graph writes them in place (no host-side mirror copies).
     bool host_direct = false;
     float *host_state = nullptr, *host_norm = nullptr;
-    // PLAMO_HIP_LAYER_LAUNCH=1: each decode layer as one phase-chained launch
-    // where the shapes allow. Off by default: on MI355X at C4 the in-launch
-    // phase barriers cost as much as launch boundaries, and blocks waiting at
-    // a barrier hold the CU slots the next phase would prefetch into.
-    bool layer_launch = false;
+    // The device's error word of the last call, copied by the call's last
+    // kernel (or a copy) into pinned host memory; status_dev is its device view.
+    uint32_t *status_host = nullptr, *status_dev = nullptr;
     // Prompt / candidate workspace (grown on demand).
     uint64_t prompt_rows = 0;
     Buffer p_state, p_norm, p_qkv, p_q, p_attn, p_branch, p_gu, p_act, p_side_k, p_side_v,
@@ -264,6 +266,55 @@ int add_range(plamo_metal *m, const void *host, uint64_t bytes) {
 }
 
 // ---------------------------------------------------------------- model setup
+// Candidate buffers of verify/commit. All or nothing: v_state is set only
+// when every buffer exists, so a later call never runs on a partial set.
+void free_verify(plamo_metal *m) {
+    for (float **p : {&m->v_state, &m->v_norm, &m->v_logits, &m->v_prop}) {
+        dev_free(m, *p);
+        *p = nullptr;
+    }
+    dev_free(m, m->v_next);
+    m->v_next = nullptr;
+    dev_free(m, m->v_argmax);
+    m->v_argmax = nullptr;
+    dev_free(m, m->copy_table);
+    m->copy_table = nullptr;
+    if (m->v_host) (void)hipHostFree(m->v_host);
+    if (m->v_next_host) (void)hipHostFree(m->v_next_host);
+    if (m->copy_table_host) (void)hipHostFree(m->copy_table_host);
+    m->v_host = nullptr;
+    m->v_next_host = nullptr;
+    m->copy_table_host = nullptr;
+}
+
+bool alloc_verify(plamo_metal *m, uint64_t L, uint64_t h, uint64_t V) {
+    const uint64_t prop = L * 3 * kMaxVerify * m->max_width;
+    float *state = dev_alloc<float>(m, kMaxVerify * h);
+    m->v_norm = dev_alloc<float>(m, kMaxVerify * h);
+    m->v_logits = dev_alloc<float>(m, kMaxVerify * V);
+    m->v_prop = dev_alloc<float>(m, prop);
+    m->v_next = dev_alloc<uint32_t>(m, kMaxVerify);
+    m->v_argmax = dev_alloc<char>(m, argmax_scratch_bytes(kMaxVerify));
+    m->copy_table = dev_alloc<CopyRow>(m, 3 * kMaxLayers);
+    bool ok = state && m->v_norm && m->v_logits && m->v_prop && m->v_next && m->v_argmax &&
+              m->copy_table;
+    ok = ok && hipHostMalloc((void **)&m->v_host, (kMaxVerify * (2 * h + V) + prop) * 4,
+                             hipHostMallocDefault) == hipSuccess;
+    ok = ok && hipHostMalloc((void **)&m->v_next_host, kMaxVerify * 4, hipHostMallocDefault) ==
+                   hipSuccess;
+    ok = ok && hipHostMalloc((void **)&m->copy_table_host, 3 * kMaxLayers * sizeof(CopyRow),
+                             hipHostMallocDefault) == hipSuccess;
+    if (!ok) {
+        (void)hipGetLastError();
+        dev_free(m, state);
+        free_verify(m);
+        problem(m, "cannot allocate verification buffers");
+        return false;
+    }
+    m->v_state = state;
+    return true;
+}
+
 void release_model(plamo_metal *m) {
     if (m->graph) {
         (void)hipGraphExecDestroy(m->graph);
@@ -284,22 +335,10 @@ void release_model(plamo_metal *m) {
     dev_free(m, m->final_norm);
     m->final_norm = nullptr;
     m->model = nullptr;
+    m->fingerprint.clear();
     m->head = m->embedding = nullptr;
     m->prompt_rows = 0;
-    for (float **p : {&m->v_state, &m->v_norm, &m->v_logits, &m->v_prop}) {
-        dev_free(m, *p);
-        *p = nullptr;
-    }
-    dev_free(m, m->v_next);
-    m->v_next = nullptr;
-    dev_free(m, m->copy_table);
-    m->copy_table = nullptr;
-    if (m->v_host) (void)hipHostFree(m->v_host);
-    if (m->v_next_host) (void)hipHostFree(m->v_next_host);
-    if (m->copy_table_host) (void)hipHostFree(m->copy_table_host);
-    m->v_host = nullptr;
-    m->v_next_host = nullptr;
-    m->copy_table_host = nullptr;
+    free_verify(m);
     m->verification_tokens = 0;
     ++m->epoch;
 }
@@ -377,8 +416,33 @@ void find_host_views(plamo_metal *m, struct model *model) {
     m->host_direct = ok;
 }
 
+std::vector<uintptr_t> model_fingerprint(const struct model *model) {
+    std::vector<uintptr_t> f;
+    if (!model) return f;
+    f = {(uintptr_t)model->count, (uintptr_t)model->hidden, (uintptr_t)model->vocab,
+         (uintptr_t)model->state, (uintptr_t)model->normalized, (uintptr_t)model->logits,
+         (uintptr_t)model->embedding, (uintptr_t)model->head, (uintptr_t)model->norm};
+    if (model->count > kMaxLayers || !model->layers) return f;
+    for (uint64_t i = 0; i < model->count; ++i) {
+        const struct layer *l = model->layers[i];
+        if (!l || !l->mixer || !l->mixer->cache || !l->mixer->rotation || !l->mixer->qkv ||
+            !l->mlp) {
+            f.push_back(0);
+            continue;
+        }
+        const struct cache *c = l->mixer->cache;
+        f.insert(f.end(), {(uintptr_t)c->k, (uintptr_t)c->v, (uintptr_t)l->mixer->rotation->out,
+                           (uintptr_t)c->capacity, (uintptr_t)c->width, (uintptr_t)c->sliding,
+                           (uintptr_t)l->mixer->qkv->weight, (uintptr_t)l->mixer->weight,
+                           (uintptr_t)l->mlp->gu, (uintptr_t)l->mlp->down,
+                           (uintptr_t)l->mlp->intermediate, (uintptr_t)l->mixer->rotation->freq});
+    }
+    return f;
+}
+
 int prepare(plamo_metal *m, struct model *model) {
-    if (m->model == model) return 1;
+    std::vector<uintptr_t> f = model_fingerprint(model);
+    if (m->model == model && f == m->fingerprint) return 1;
     release_model(m);
     if (!model || !model->count || model->count > kMaxLayers || !model->hidden ||
         model->hidden > UINT32_MAX || !model->vocab || model->vocab > UINT32_MAX ||
@@ -470,7 +534,7 @@ int prepare(plamo_metal *m, struct model *model) {
             return 0;
         }
         d.synced = false;
-        d.last_k.assign(d.width, 0.0f);
+        d.last_kv.assign(2 * (size_t)d.width, 0.0f);
         m->max_width = std::max<uint64_t>(m->max_width, d.width);
         m->max_qkv = std::max<uint64_t>(m->max_qkv, (uint64_t)(d.qh + 2 * d.kh) * d.dim);
         m->max_attention = std::max<uint64_t>(m->max_attention, (uint64_t)d.qh * d.dim);
@@ -512,7 +576,6 @@ int prepare(plamo_metal *m, struct model *model) {
     dev_free(m, m->down_out);
     dev_free(m, m->partial);
     dev_free(m, m->counters);
-    dev_free(m, m->layer_counters);
     dev_free(m, m->outbox);
     if (m->outbox_host) (void)hipHostFree(m->outbox_host);
     m->outbox_host = nullptr;
@@ -526,20 +589,19 @@ int prepare(plamo_metal *m, struct model *model) {
     m->down_out = dev_alloc<float>(m, h);
     m->partial = dev_alloc<float>(m, m->max_partial * m->max_splits);
     m->counters = dev_alloc<uint32_t>(m, 256);
-    m->layer_counters = dev_alloc<uint32_t>(m, L * kLayerCounterWords);
     m->outbox_floats = V + 2 * h + L * 3 * m->max_width;
     m->outbox = dev_alloc<float>(m, m->outbox_floats);
     if (!m->state_a || !m->state_b || !m->qkv || !m->q || !m->attn || !m->branch || !m->act ||
-        !m->down_out || !m->partial || !m->counters || !m->layer_counters || !m->outbox ||
+        !m->down_out || !m->partial || !m->counters || !m->outbox ||
         hipHostMalloc((void **)&m->outbox_host, m->outbox_floats * 4, hipHostMallocDefault) !=
             hipSuccess ||
-        hipMemset(m->counters, 0, 256 * 4) != hipSuccess ||
-        hipMemset(m->layer_counters, 0, L * kLayerCounterWords * 4) != hipSuccess) {
+        hipMemset(m->counters, 0, 256 * 4) != hipSuccess) {
         (void)hipGetLastError();
         release_model(m);
         return problem(m, "cannot allocate decode workspace");
     }
     m->model = model;
+    m->fingerprint = std::move(f);
     find_host_views(m, model);
     ++m->epoch;
     return 1;
@@ -578,10 +640,12 @@ int sync_from_host(plamo_metal *m, struct model *model, std::vector<char> &stale
         const struct cache *c = mx->cache;
         const struct rotation *r = mx->rotation;
         uint32_t scale = float_bits(model->scales[i]);
+        const uint64_t last = c->count ? (c->count - 1) * c->width : 0;
         bool same = d.synced && d.count == c->count && d.processed == r->processed_count &&
                     d.scale_bits == r->scale_bits &&
-                    (!c->count || !memcmp(c->k + (c->count - 1) * c->width, d.last_k.data(),
-                                          c->width * 4));
+                    (!c->count ||
+                     (!memcmp(c->k + last, d.last_kv.data(), c->width * 4) &&
+                      !memcmp(c->v + last, d.last_kv.data() + c->width, c->width * 4)));
         if (same) {
             stale[i] = r->processed_count != c->count || r->scale_bits != scale;
             continue;
@@ -609,7 +673,10 @@ void remember(plamo_metal *m, struct model *model) {
         d.count = c->count;
         d.processed = mx->rotation->processed_count;
         d.scale_bits = mx->rotation->scale_bits;
-        if (c->count) memcpy(d.last_k.data(), c->k + (c->count - 1) * c->width, c->width * 4);
+        if (c->count) {
+            memcpy(d.last_kv.data(), c->k + (c->count - 1) * c->width, c->width * 4);
+            memcpy(d.last_kv.data() + c->width, c->v + (c->count - 1) * c->width, c->width * 4);
+        }
         d.synced = true;
     }
 }
@@ -622,6 +689,14 @@ int end_timing(plamo_metal *m) {
     if (hipEventElapsedTime(&ms, m->start, m->stop) == hipSuccess) m->info.gpu_seconds += ms * 1e-3;
     ++m->info.command_buffers;
     return 1;
+}
+
+// A kernel of the call gave up a bounded wait (runtime/metal.h:63-67: the
+// call then fails with -1 after partial writes).
+bool device_failed(plamo_metal *m) {
+    if (!*m->status_host) return false;
+    problem(m, "a bounded device wait gave up (error word %u)", *m->status_host);
+    return true;
 }
 
 // ---------------------------------------------------------------- decode
@@ -641,9 +716,7 @@ int encode_decode(plamo_metal *m, struct model *model, const DecodePlan &plan, i
     float *stage = m->outbox + V + 2 * h;
     HIP_TRY(m, hipMemcpyAsync(m->params_dev, m->params_host, sizeof(StepParams),
                               hipMemcpyHostToDevice, s));
-    // The embedding launch also zeroes the one-launch layers' phase counters.
-    HIP_TRY(m, launch_embed(s, m->embedding, nullptr, m->params_dev, 1, (uint32_t)h, m->state_a,
-                            m->layer_counters, (uint32_t)(L * kLayerCounterWords / kLaneStride)));
+    HIP_TRY(m, launch_embed(s, m->embedding, nullptr, m->params_dev, 1, (uint32_t)h, m->state_a));
     ++n;
     float *cur = m->state_a, *nxt = m->state_b;
     const int blocks = 2 * m->cus;
@@ -694,47 +767,6 @@ int encode_decode(plamo_metal *m, struct model *model, const DecodePlan &plan, i
             da.splits = decode_attention_splits(d.rows);
             return da;
         };
-        if (!shift && d.fused && m->layer_launch) {
-            // The rotated rows are refreshed first (they do not depend on
-            // this step's projections).
-            LayerStep ls{};
-            ls.qkv_w = d.qkv;
-            ls.pq = p1;
-            ls.qkv = m->qkv;
-            ls.qkv_rows = (uint32_t)qkv_rows;
-            ls.a = attention_args();
-            ls.o_w = d.o;
-            ls.branch = m->branch;
-            ls.gu_w = d.gu;
-            ls.act = m->act;
-            ls.down_w = d.down;
-            ls.down_out = m->down_out;
-            ls.hidden = (uint32_t)h;
-            ls.inter = d.inter;
-            ls.phase = m->layer_counters + i * kLayerCounterWords;
-            ls.error = &m->params_dev->error;
-            float *in = cur, *out = nxt;
-            if (i) std::swap(in, out);
-            ls.pg.src = in;
-            ls.pg.w = mpre;
-            ls.pg.offset = 1.0f;
-            ls.pg.branch = m->branch;
-            ls.pg.rw = post;
-            ls.pg.roffset = kAttentionOffset;
-            ls.pg.state_out = out;
-            if (layer_plan(ls, (uint32_t)blocks)) {
-                if (stale) {
-                    uint32_t rows = m->params_host->count[i];
-                    HIP_TRY(m, launch_rerotate(s, d.k, d.rot, rope.table, rows, d.kh, d.dim));
-                    ++n;
-                }
-                HIP_TRY(m, launch_layer(s, ls));
-                ++n;
-                cur = out;
-                nxt = in;
-                continue;
-            }
-        }
         HIP_TRY(m, launch_gemv(s, d.qkv, qkv_rows, h, p1, m->qkv, 0, blocks));
         ++n;
         if (i) std::swap(cur, nxt);
@@ -848,6 +880,8 @@ int encode_decode(plamo_metal *m, struct model *model, const DecodePlan &plan, i
     ph.roffset = kMlpOffset;
     ph.state_out = plan.direct ? m->host_state : state_out;
     ph.norm_out = plan.direct ? m->host_norm : norm_out;
+    ph.status = &m->params_dev->error;
+    ph.status_out = m->status_dev;
     HIP_TRY(m, launch_gemv(s, m->head, V, h, ph, logits, 0, blocks));
     ++n;
     if (plan.direct)
@@ -980,7 +1014,6 @@ struct plamo_metal *plamo_metal_open(const struct plamo_metal_config *config, ch
         return nullptr;
     }
     m->cus = prop.multiProcessorCount;
-    if (const char *e = getenv("PLAMO_HIP_LAYER_LAUNCH")) m->layer_launch = atoi(e) != 0;
     snprintf(m->info.device, sizeof m->info.device, "%s (%s, %d CUs)", prop.name,
              prop.gcnArchName, prop.multiProcessorCount);
     snprintf(m->info.precision, sizeof m->info.precision, "fp32");
@@ -990,6 +1023,8 @@ struct plamo_metal *plamo_metal_open(const struct plamo_metal_config *config, ch
         hipEventCreate(&m->start) != hipSuccess || hipEventCreate(&m->stop) != hipSuccess ||
         hipHostMalloc((void **)&m->params_host, sizeof(StepParams), hipHostMallocDefault) !=
             hipSuccess ||
+        hipHostMalloc((void **)&m->status_host, 64, hipHostMallocDefault) != hipSuccess ||
+        !(m->status_dev = (uint32_t *)device_view(m->status_host)) ||
         hipMalloc((void **)&m->params_dev, sizeof(StepParams)) != hipSuccess) {
         (void)hipGetLastError();
         if (error && cap) snprintf(error, cap, "cannot create HIP stream or staging");
@@ -997,6 +1032,7 @@ struct plamo_metal *plamo_metal_open(const struct plamo_metal_config *config, ch
         return nullptr;
     }
     memset(m->params_host, 0, sizeof(StepParams));
+    *m->status_host = 0;
     if (m->config.memory != PLAMO_METAL_STREAM)
         for (size_t i = 0; i < m->config.count && m->config.maps; ++i)
             if (!add_range(m, m->config.maps[i].base, m->config.maps[i].bytes)) {
@@ -1044,6 +1080,7 @@ void plamo_metal_close(struct plamo_metal *m) {
     if (m->v_next_host) (void)hipHostFree(m->v_next_host);
     if (m->copy_table_host) (void)hipHostFree(m->copy_table_host);
     if (m->params_host) (void)hipHostFree(m->params_host);
+    if (m->status_host) (void)hipHostFree(m->status_host);
     if (m->params_dev) (void)hipFree(m->params_dev);
     if (m->start) (void)hipEventDestroy(m->start);
     if (m->stop) (void)hipEventDestroy(m->stop);
@@ -1106,6 +1143,7 @@ int plamo_metal_forward(struct plamo_metal *m, struct model *model, uint64_t tok
     if (plan.special && (!ensure_prompt(m, model, 1) || !ensure_window_scratch(m, model))) return -1;
     m->params_host->token = (uint32_t)token;
     m->params_host->tokens = 1;
+    *m->status_host = 0;
     plan.direct = m->host_direct && !plan.special;
     int dispatches = 0;
     begin_timing(m);
@@ -1138,6 +1176,7 @@ int plamo_metal_forward(struct plamo_metal *m, struct model *model, uint64_t tok
     }
     if (!end_timing(m)) return fail(m);
     m->info.dispatches += dispatches;
+    if (device_failed(m)) return fail(m);
     // Host mirror (runtime/metal_model.m:491-500); a direct step has written
     // logits, state, normalized and the new rows in place already.
     const float *out = m->outbox_host;
@@ -1210,30 +1249,7 @@ int run_prompt(plamo_metal *m, struct model *model, const uint32_t *ids, uint64_
     const GemmWorkspace *ws =
         gemm_workspace(m, T, std::max({h, m->max_attention, m->max_inter}));
     if (!ws) return -1;
-    if (verify) {
-        uint64_t prop = L * 3 * kMaxVerify * m->max_width;
-        if (!m->v_state) {
-            m->v_state = dev_alloc<float>(m, kMaxVerify * h);
-            m->v_norm = dev_alloc<float>(m, kMaxVerify * h);
-            m->v_logits = dev_alloc<float>(m, kMaxVerify * V);
-            m->v_prop = dev_alloc<float>(m, prop);
-            m->v_next = dev_alloc<uint32_t>(m, kMaxVerify);
-            m->v_argmax = dev_alloc<char>(m, argmax_scratch_bytes(kMaxVerify));
-            m->copy_table = dev_alloc<CopyRow>(m, 3 * kMaxLayers);
-            if (!m->v_state || !m->v_norm || !m->v_logits || !m->v_prop || !m->v_next ||
-                !m->v_argmax ||
-                !m->copy_table ||
-                hipHostMalloc((void **)&m->v_host, (kMaxVerify * (2 * h + V) + prop) * 4,
-                              hipHostMallocDefault) != hipSuccess ||
-                hipHostMalloc((void **)&m->v_next_host, kMaxVerify * 4, hipHostMallocDefault) !=
-                    hipSuccess ||
-                hipHostMalloc((void **)&m->copy_table_host, 3 * kMaxLayers * sizeof(CopyRow),
-                              hipHostMallocDefault) != hipSuccess) {
-                (void)hipGetLastError();
-                return problem(m, "cannot allocate verification buffers") - 1;
-            }
-        }
-    }
+    if (verify && !m->v_state && !alloc_verify(m, L, h, V)) return -1;
     std::vector<char> overflow(L, 0);
     uint64_t split_floats = 0;
     for (uint64_t i = 0; i < L; ++i) {
@@ -1252,6 +1268,7 @@ int run_prompt(plamo_metal *m, struct model *model, const uint32_t *ids, uint64_
         m->params_host->count[i] = (uint32_t)c->count;
     }
     m->params_host->tokens = (uint32_t)T;
+    *m->status_host = 0;
     memcpy(m->ids_host, ids, T * 4);
     hipStream_t s = m->stream;
     int n = 0;
@@ -1424,6 +1441,7 @@ int run_prompt(plamo_metal *m, struct model *model, const uint32_t *ids, uint64_
         HIP_FAIL(m, hipMemcpyAsync(m->v_host + kMaxVerify * (2 * h + V), m->v_prop,
                                   L * 3 * kMaxVerify * m->max_width * 4, hipMemcpyDeviceToHost, s));
         HIP_FAIL(m, hipMemcpyAsync(m->v_next_host, m->v_next, T * 4, hipMemcpyDeviceToHost, s));
+        HIP_FAIL(m, hipMemcpyAsync(m->status_host, &m->params_dev->error, 4, hipMemcpyDeviceToHost, s));
         n += 3;
     } else {
         const float *last = state + (T - 1) * h;
@@ -1432,6 +1450,8 @@ int run_prompt(plamo_metal *m, struct model *model, const uint32_t *ids, uint64_
         ph.w = m->final_norm;
         ph.offset = 1.0f;
         ph.norm_out = m->outbox + V + h;
+        ph.status = &m->params_dev->error;
+        ph.status_out = m->status_dev;
         HIP_FAIL(m, launch_gemv(s, m->head, V, h, ph, m->outbox, 0, 2 * m->cus));
         HIP_FAIL(m, hipMemcpyAsync(m->outbox + V, last, h * 4, hipMemcpyDeviceToDevice, s));
         HIP_FAIL(m, hipMemcpyAsync(m->outbox_host, m->outbox, (V + 2 * h) * 4,
@@ -1440,6 +1460,7 @@ int run_prompt(plamo_metal *m, struct model *model, const uint32_t *ids, uint64_
     }
     if (!end_timing(m)) return fail(m);
     m->info.dispatches += n;
+    if (device_failed(m)) return fail(m);
     if (verify) {
         m->verification_tokens = T;
         m->verification_index = 0;
@@ -1702,6 +1723,17 @@ int plamo_metal_mlp(struct plamo_metal *m, const struct mlp *mlp, float *states,
 }
 
 }  // extern "C"
+
+extern "C" void plamo_hip_invalidate(struct plamo_metal *m) {
+    if (!m) return;
+    for (Layer &l : m->layers) l.synced = false;
+}
+
+extern "C" void plamo_hip_debug_waits(struct plamo_metal *m, uint32_t extra, uint32_t polls) {
+    if (!m) return;
+    m->params_host->wait_extra = extra;
+    m->params_host->wait_limit = polls;
+}
 
 extern "C" int plamo_hip_time_kernel(struct plamo_metal *m, struct model *model, uint64_t layer,
                                      int which, int reps, double *ms_per_launch,

@@ -18,7 +18,12 @@ struct StepParams {
     uint32_t tokens;            // prompt / candidate rows of this call
     uint32_t count[kMaxLayers]; // cache rows of each layer before this call
     uint32_t done[kMaxLayers];  // fused attention: finished KV heads (zero at launch)
-    uint32_t error;             // fused attention: a wait gave up
+    uint32_t error;             // fused attention: a wait gave up (zero at launch)
+    // Bounded wait of the fused attention's O blocks: the target is the KV
+    // heads plus wait_extra, polled at most wait_limit times (0: 2^22).
+    // Both are zero outside tests, which raise them from the host so that a
+    // wait gives up and the failure path runs with every kernel exiting.
+    uint32_t wait_extra, wait_limit;
 };
 
 // Norm applied in a GEMV prologue: x = rms(src) * (bf16(w) + offset).
@@ -33,20 +38,16 @@ struct Prologue {
     float roffset;
     float *state_out;        // written by block 0 when branch != nullptr
     float *norm_out;         // written by block 0 when non-null (normalized x)
+    // Block 0 copies *status to *status_out when non-null (the decode head
+    // hands the step's error word to a pinned host word this way).
+    const uint32_t *status;
+    uint32_t *status_out;
 };
 
 hipError_t launch_rope_table(hipStream_t, const float *freq, float scale, uint32_t half,
                              uint64_t first_row, uint64_t rows, float *table);
-// Counters of the one-launch layer: 4 phases per layer, each kPhaseLanes
-// counters kLaneStride words apart (separate 64-byte lines).
-constexpr uint32_t kPhaseLanes = 16, kLaneStride = 16;
-constexpr uint32_t kPhaseWords = kPhaseLanes * kLaneStride;
-constexpr uint32_t kLayerCounterWords = 4 * kPhaseWords;
-// `clear` (optional): counters zeroed by the launch, clear[i * kLaneStride]
-// for i < clear_count.
 hipError_t launch_embed(hipStream_t, const uint16_t *embedding, const uint32_t *ids,
-                        const StepParams *params, uint32_t tokens, uint32_t hidden, float *out,
-                        uint32_t *clear = nullptr, uint32_t clear_count = 0);
+                        const StepParams *params, uint32_t tokens, uint32_t hidden, float *out);
 // y[r] = W[r,:] . x (x from the prologue). swiglu_half > 0: rows r and
 // r + swiglu_half are gate/up and y[r] = silu(gate) * up for r < swiglu_half.
 hipError_t launch_gemv(hipStream_t, const uint16_t *w, uint64_t rows, uint64_t cols,
@@ -167,35 +168,6 @@ bool attention_o_supported(uint32_t dim, uint32_t group, uint64_t cols);
 // Blocks per KV head that cover `rows` cache rows (DecodeAttention::splits
 // must be at least this for the largest row count of the launch).
 uint32_t decode_attention_splits(uint64_t rows);
-
-// One decoder layer of a decode step as one launch: QKV projection (norm
-// prologue, residual of the previous layer's MLP), attention with the cache
-// append, O projection, gate/up with SwiGLU (norm prologue, attention
-// residual), down projection. Blocks run in that phase order; `phase` holds
-// the layer's kLayerCounterWords counter words, zero at launch. Blocks per
-// phase: nq, the attention's kh * splits, no, ng, nd.
-struct LayerStep {
-    const uint16_t *qkv_w;
-    Prologue pq;
-    float *qkv;
-    uint32_t qkv_rows;
-    DecodeAttention a;  // a.out is the O projection's input
-    const uint16_t *o_w;
-    float *branch;      // O projection output
-    const uint16_t *gu_w;
-    Prologue pg;
-    float *act;         // SwiGLU output
-    const uint16_t *down_w;
-    float *down_out;
-    uint32_t hidden, inter;
-    uint32_t nq, no, ng, nd;
-    uint32_t *phase;
-    uint32_t *error;
-};
-// Fills the block counts; false when the layer's shapes have no fused variant
-// (the caller then launches the projections and attention separately).
-bool layer_plan(LayerStep &l, uint32_t blocks_hint);
-hipError_t launch_layer(hipStream_t, const LayerStep &);
 
 // General causal attention for `tokens` query rows. Key j of query t is the
 // virtual row j of [cache rows 0..prefix) ++ [new rows 0..tokens). With

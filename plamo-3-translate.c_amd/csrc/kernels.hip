@@ -121,68 +121,13 @@ __device__ __forceinline__ bool arrive_last(uint32_t *counter, uint32_t expected
     return *flag;
 }
 
-// Dependencies between the phases of a chained launch (blocks ordered by
-// phase; a block waits only on lower-numbered blocks, which are dispatched
-// before it and never wait on it). A gate waits until *counter >= target; the
-// wait is bounded, and a block that gives up sets *error and writes NaN
-// results (they surface as a failed argmax). A signal counts a block in after
-// its results are written through to the coherence point.
-// A phase's arrivals are spread over `lanes` counters kLaneStride words
-// apart (block b counts on lane b % lanes): hundreds of blocks finishing
-// together would otherwise queue their atomics on one address.
-struct Gate {
-    const uint32_t *counter;
-    uint32_t lanes;
-    uint32_t target;
-    uint32_t *error;
-};
-struct Signal {
-    uint32_t *counter;
-    uint32_t lanes;
-};
-// One thread polls (a block of pollers would put thousands of requests per
-// microsecond on the counter's memory channel); the barrier then releases the
-// block. The barrier waits for LDS only, so loads issued before it stay in
-// flight.
-__device__ __forceinline__ bool gate_wait(const Gate &g) {
-    if (!g.counter) return true;
-    __shared__ int gate_open;
-    if (threadIdx.x == 0) {
-        uint32_t spins = 0;
-        int open = 1;
-        auto arrived = [&]() {
-            uint32_t sum = 0;
-            for (uint32_t l = 0; l < g.lanes; ++l)
-                sum += __hip_atomic_load(const_cast<uint32_t *>(g.counter + l * kLaneStride),
-                                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            return sum;
-        };
-        while (arrived() < g.target) {
-            __builtin_amdgcn_s_sleep(2);
-            if (++spins == (1u << 22)) {
-                atomicOr(g.error, 1u);
-                open = 0;
-                break;
-            }
-        }
-        gate_open = open;
-    }
-    __syncthreads();
-    return gate_open != 0;
-}
-__device__ __forceinline__ void signal_done(const Signal &s, uint32_t bid) {
-    if (!s.counter) return;
-    wait_stores();
-    __syncthreads();
-    if (threadIdx.x == 0)
-        __hip_atomic_fetch_add(s.counter + (bid % s.lanes) * kLaneStride, 1u, __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void put(float *p, float v, bool through) {
-    if (through)
-        store_through(p, v);
-    else
-        *p = v;
+// The device's own status for the host: block 0 of a launch that carries a
+// Prologue with `status_out` copies the step's error word there (the decode
+// head, a pinned host word), so a step whose bounded wait gave up is reported
+// by the call instead of leaving NaN logits behind a success.
+__device__ __forceinline__ void publish_status(const Prologue &pro, uint32_t bid) {
+    if (bid == 0 && threadIdx.x == 0 && pro.status_out)
+        *pro.status_out = __hip_atomic_load(pro.status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // 1 / sqrt(mean(x^2) + 1e-6) for a 256-thread block (tests/rmsnorm_reference.s:8-21
@@ -280,13 +225,8 @@ hipError_t launch_rope_table(hipStream_t stream, const float *freq, float scale,
 __global__ __launch_bounds__(kThreads) void embed_kernel(const uint16_t *embedding,
                                                          const uint32_t *ids,
                                                          const StepParams *params,
-                                                         uint32_t hidden, float *out,
-                                                         uint32_t *clear, uint32_t clear_count) {
+                                                         uint32_t hidden, float *out) {
     uint32_t t = blockIdx.y;
-    if (clear && t == 0)
-        for (uint32_t i = blockIdx.x * kThreads + threadIdx.x; i < clear_count;
-             i += gridDim.x * kThreads)
-            clear[(uint64_t)i * kLaneStride] = 0;
     uint32_t id = ids ? ids[t] : params->token;
     const uint16_t *row = embedding + (uint64_t)id * hidden;
     float *o = out + (uint64_t)t * hidden;
@@ -295,12 +235,10 @@ __global__ __launch_bounds__(kThreads) void embed_kernel(const uint16_t *embeddi
 }
 
 hipError_t launch_embed(hipStream_t stream, const uint16_t *embedding, const uint32_t *ids,
-                        const StepParams *params, uint32_t tokens, uint32_t hidden, float *out,
-                        uint32_t *clear, uint32_t clear_count) {
+                        const StepParams *params, uint32_t tokens, uint32_t hidden, float *out) {
     unsigned bx = (hidden + kThreads - 1) / kThreads;
     if (bx > 16) bx = 16;
-    embed_kernel<<<dim3(bx, tokens), kThreads, 0, stream>>>(embedding, ids, params, hidden, out,
-                                                            clear, clear_count);
+    embed_kernel<<<dim3(bx, tokens), kThreads, 0, stream>>>(embedding, ids, params, hidden, out);
     return hipGetLastError();
 }
 
@@ -353,17 +291,16 @@ __device__ __forceinline__ void gemv_accumulate(const float *xs, uint64_t chunks
 
 template <bool SWIGLU>
 __device__ __forceinline__ void gemv_store(float *y, uint64_t rows, uint64_t pair, float acc_a,
-                                           float acc_b, uint32_t lane, bool through, bool ok) {
+                                           float acc_b, uint32_t lane) {
     acc_a = wave_sum(acc_a);
     acc_b = wave_sum(acc_b);
-    if (!ok) acc_a = acc_b = __builtin_nanf("");
     if (lane == 0) {
         if (SWIGLU) {
             float d = plamo_exp(-acc_a) + 1.0f;
-            put(y + pair, (acc_a / d) * acc_b, through);
+            y[pair] = (acc_a / d) * acc_b;
         } else {
-            put(y + 2 * pair, acc_a, through);
-            if (2 * pair + 1 < rows) put(y + 2 * pair + 1, acc_b, through);
+            y[2 * pair] = acc_a;
+            if (2 * pair + 1 < rows) y[2 * pair + 1] = acc_b;
         }
     }
 }
@@ -373,7 +310,7 @@ __device__ __forceinline__ void gemv_store(float *y, uint64_t rows, uint64_t pai
 // thread a contiguous 16-element slice: its loads go out in one batch, then
 // two block reductions. prologue_load issues the loads, prologue_finish
 // writes the normalized vector to LDS (and block 0 the optional state/norm
-// copies, written through when another block of the launch reads them).
+// copies).
 struct ProloguePart {
     float sv[16], bv[16], wv[16], rv[16];
     uint32_t i0;
@@ -423,8 +360,7 @@ __device__ __forceinline__ void prologue_load(const Prologue &pro, ProloguePart 
     }
 }
 __device__ __forceinline__ void prologue_finish(const Prologue &pro, uint32_t n, ProloguePart &pp,
-                                                float *xs, float *red, uint32_t bid,
-                                                bool through) {
+                                                float *xs, float *red, uint32_t bid) {
     if (pp.fast) {
         float ss = 0.0f;
         if (pro.branch) {
@@ -442,16 +378,11 @@ __device__ __forceinline__ void prologue_finish(const Prologue &pro, uint32_t n,
                     float scale = pp.rv[k] + pro.roffset;
                     pp.sv[k] = pp.sv[k] + b * scale;
                 }
-            if (bid == 0 && pro.state_out && pp.mine) {
-                if (through)
+            if (bid == 0 && pro.state_out && pp.mine)
 #pragma unroll
-                    for (int k = 0; k < 16; ++k) store_through(pro.state_out + pp.i0 + k, pp.sv[k]);
-                else
-#pragma unroll
-                    for (int q = 0; q < 4; ++q)
-                        *(f32x4 *)(pro.state_out + pp.i0 + 4 * q) =
-                            f32x4{pp.sv[4 * q], pp.sv[4 * q + 1], pp.sv[4 * q + 2], pp.sv[4 * q + 3]};
-            }
+                for (int q = 0; q < 4; ++q)
+                    *(f32x4 *)(pro.state_out + pp.i0 + 4 * q) =
+                        f32x4{pp.sv[4 * q], pp.sv[4 * q + 1], pp.sv[4 * q + 2], pp.sv[4 * q + 3]};
             ss = 0.0f;
         }
         if (pp.mine)
@@ -470,16 +401,7 @@ __device__ __forceinline__ void prologue_finish(const Prologue &pro, uint32_t n,
                 x.z = (pp.sv[4 * q + 2] * is) * (pp.wv[4 * q + 2] + pro.offset);
                 x.w = (pp.sv[4 * q + 3] * is) * (pp.wv[4 * q + 3] + pro.offset);
                 *(f32x4 *)(xs + pp.i0 + 4 * q) = x;
-                if (bid == 0 && pro.norm_out) {
-                    if (through) {
-                        store_through(pro.norm_out + pp.i0 + 4 * q, x.x);
-                        store_through(pro.norm_out + pp.i0 + 4 * q + 1, x.y);
-                        store_through(pro.norm_out + pp.i0 + 4 * q + 2, x.z);
-                        store_through(pro.norm_out + pp.i0 + 4 * q + 3, x.w);
-                    } else {
-                        *(f32x4 *)(pro.norm_out + pp.i0 + 4 * q) = x;
-                    }
-                }
+                if (bid == 0 && pro.norm_out) *(f32x4 *)(pro.norm_out + pp.i0 + 4 * q) = x;
             }
         __syncthreads();
     } else if (!pro.w) {
@@ -499,7 +421,7 @@ __device__ __forceinline__ void prologue_finish(const Prologue &pro, uint32_t n,
         }
         __syncthreads();
         if (pro.branch && bid == 0 && pro.state_out)
-            for (uint32_t i = threadIdx.x; i < n; i += kThreads) put(pro.state_out + i, xs[i], through);
+            for (uint32_t i = threadIdx.x; i < n; i += kThreads) pro.state_out[i] = xs[i];
         float is = block_rms_inverse(xs, n, red);
         for (uint32_t i = threadIdx.x; i < n; i += kThreads) {
             float scale = bf16f(pro.w[i]) + pro.offset;
@@ -507,7 +429,7 @@ __device__ __forceinline__ void prologue_finish(const Prologue &pro, uint32_t n,
         }
         __syncthreads();
         if (bid == 0 && pro.norm_out)
-            for (uint32_t i = threadIdx.x; i < n; i += kThreads) put(pro.norm_out + i, xs[i], through);
+            for (uint32_t i = threadIdx.x; i < n; i += kThreads) pro.norm_out[i] = xs[i];
     }
 }
 
@@ -518,19 +440,14 @@ __device__ __forceinline__ void prologue_finish(const Prologue &pro, uint32_t n,
 // keeps three batches in flight: batch i+3 is requested as batch i is consumed.
 // With SWIGLU the pair is (gate row r, up row r+half) and the output is
 // silu(gate) * up (tests/activation_reference.s:99-126).
-// One block (index bid of nblocks) of the LDS-input GEMV. With a gate the
-// weight batches go out first and the prologue's inputs are read after the
-// wait; with a signal the results are written through and the block counted.
 template <bool VEC, bool SWIGLU>
-__device__ __forceinline__ void gemv_block(const uint16_t *__restrict__ w, uint64_t rows,
-                                           uint64_t cols, const Prologue &pro,
-                                           float *__restrict__ y, uint64_t half, uint32_t bid,
-                                           uint32_t nblocks, const Gate &gate,
-                                           const Signal &sig) {
+__global__ __launch_bounds__(kThreads) void gemv_kernel(const uint16_t *__restrict__ w,
+                                                        uint64_t rows, uint64_t cols,
+                                                        Prologue pro, float *__restrict__ y,
+                                                        uint64_t half) {
     extern __shared__ float xs[];
     __shared__ float red[4];
-    const bool through = sig.counter != nullptr;
-    bool ok = true;
+    const uint32_t bid = blockIdx.x, nblocks = gridDim.x;
     const uint32_t n = (uint32_t)cols;
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const uint64_t pairs = SWIGLU ? half : (rows + 1) / 2;
@@ -541,7 +458,7 @@ __device__ __forceinline__ void gemv_block(const uint16_t *__restrict__ w, uint6
     const uint64_t total = p0 < pairs ? ((pairs - 1 - p0) / step + 1) * nb : 0;
     ProloguePart pp;
     prologue_begin(pro, n, pp);
-    if (!gate.counter) prologue_load(pro, pp);
+    prologue_load(pro, pp);
     __builtin_amdgcn_sched_barrier(0);
     // Three batches in flight: the first three go out before the prologue.
     u32x4 qa0[4], qb0[4], qa1[4], qb1[4], qa2[4], qb2[4];
@@ -555,18 +472,15 @@ __device__ __forceinline__ void gemv_block(const uint16_t *__restrict__ w, uint6
         if (total > 2) issue(2, qa2, qb2);
     }
     __builtin_amdgcn_sched_barrier(0);
-    if (gate.counter) {
-        ok = gate_wait(gate);
-        prologue_load(pro, pp);
-    }
-    prologue_finish(pro, n, pp, xs, red, bid, through);
+    prologue_finish(pro, n, pp, xs, red, bid);
+    publish_status(pro, bid);
 
     if (VEC) {
         float acc_a = 0.0f, acc_b = 0.0f;
         auto consume = [&](uint64_t it, const u32x4(&qa)[4], const u32x4(&qb)[4]) {
             gemv_accumulate(xs, chunks, lane + (it % nb) * 256, qa, qb, acc_a, acc_b);
             if (it % nb == nb - 1) {
-                gemv_store<SWIGLU>(y, rows, p0 + (it / nb) * step, acc_a, acc_b, lane, through, ok);
+                gemv_store<SWIGLU>(y, rows, p0 + (it / nb) * step, acc_a, acc_b, lane);
                 acc_a = acc_b = 0.0f;
             }
         };
@@ -604,18 +518,9 @@ __device__ __forceinline__ void gemv_block(const uint16_t *__restrict__ w, uint6
                 acc_a = __builtin_fmaf(bf16f(wa[k]), xs[k], acc_a);
                 acc_b = __builtin_fmaf(bf16f(wb[k]), xs[k], acc_b);
             }
-            gemv_store<SWIGLU>(y, rows, p, acc_a, acc_b, lane, through, ok);
+            gemv_store<SWIGLU>(y, rows, p, acc_a, acc_b, lane);
         }
     }
-    signal_done(sig, bid);
-}
-
-template <bool VEC, bool SWIGLU>
-__global__ __launch_bounds__(kThreads) void gemv_kernel(const uint16_t *__restrict__ w,
-                                                        uint64_t rows, uint64_t cols,
-                                                        Prologue pro, float *__restrict__ y,
-                                                        uint64_t half) {
-    gemv_block<VEC, SWIGLU>(w, rows, cols, pro, y, half, blockIdx.x, gridDim.x, Gate{}, Signal{});
 }
 
 // Raw-input projections (attention output, MLP down): each lane keeps its
@@ -623,13 +528,13 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(const uint16_t *__restri
 // columns, and a wave streams U rows at a time. No LDS staging of x, so the
 // 16K-column down projection is not occupancy-limited by LDS.
 template <int KC, int WPR, int U>
-__device__ __forceinline__ void reg_block(const uint16_t *__restrict__ w, uint64_t rows,
-                                          uint64_t cols, const float *__restrict__ src,
-                                          float *__restrict__ y, uint32_t bid, uint32_t nblocks,
-                                          const Gate &gate, const Signal &sig) {
+__global__ __launch_bounds__(kThreads) void gemv_reg_kernel(const uint16_t *__restrict__ w,
+                                                            uint64_t rows, uint64_t cols,
+                                                            const float *__restrict__ src,
+                                                            float *__restrict__ y) {
     constexpr int GROUPS = 4 / WPR;
     __shared__ float part[4][U];
-    const bool through = sig.counter != nullptr;
+    const uint32_t bid = blockIdx.x, nblocks = gridDim.x;
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const uint32_t pidx = wave % WPR, grp = wave / WPR;
     const uint64_t col0 = (uint64_t)pidx * KC * 512 + lane * 8;
@@ -648,7 +553,6 @@ __device__ __forceinline__ void reg_block(const uint16_t *__restrict__ w, uint64
     };
     const uint64_t ubase = (uint64_t)bid * GROUPS;
     if (ubase + grp < units) load(ubase + grp);
-    const bool ok = gate_wait(gate);
     float x[KC][8];
 #pragma unroll
     for (int c = 0; c < KC; ++c) {
@@ -674,13 +578,13 @@ __device__ __forceinline__ void reg_block(const uint16_t *__restrict__ w, uint64
                     a = __builtin_fmaf(__uint_as_float(q[e] & 0xffff0000u), x[c][2 * e + 1], a);
                 }
             }
-            acc[u] = ok ? wave_sum(a) : __builtin_nanf("");
+            acc[u] = wave_sum(a);
         }
         if (WPR == 1) {
             if (lane == 0 && valid)
 #pragma unroll
                 for (int u = 0; u < U; ++u)
-                    if (unit * U + u < rows) put(y + unit * U + u, acc[u], through);
+                    if (unit * U + u < rows) y[unit * U + u] = acc[u];
         } else {
             if (lane == 0)
 #pragma unroll
@@ -692,20 +596,11 @@ __device__ __forceinline__ void reg_block(const uint16_t *__restrict__ w, uint64
                     float t = part[wave][u];
 #pragma unroll
                     for (int q = 1; q < WPR; ++q) t += part[wave + q][u];
-                    if (unit * U + u < rows) put(y + unit * U + u, t, through);
+                    if (unit * U + u < rows) y[unit * U + u] = t;
                 }
             __syncthreads();
         }
     }
-    signal_done(sig, bid);
-}
-
-template <int KC, int WPR, int U>
-__global__ __launch_bounds__(kThreads) void gemv_reg_kernel(const uint16_t *__restrict__ w,
-                                                            uint64_t rows, uint64_t cols,
-                                                            const float *__restrict__ src,
-                                                            float *__restrict__ y) {
-    reg_block<KC, WPR, U>(w, rows, cols, src, y, blockIdx.x, gridDim.x, Gate{}, Signal{});
 }
 
 // Decode projections with a norm prologue, x held in registers: the block
@@ -715,11 +610,10 @@ __global__ __launch_bounds__(kThreads) void gemv_reg_kernel(const uint16_t *__re
 // p + half) and the output silu(gate) * up (tests/activation_reference.s:99-126).
 // The first rows' weights are requested before the prologue's reductions.
 template <int KC, int U, bool SWIGLU, int WPR = 1>
-__device__ __forceinline__ void regp_block(const uint16_t *__restrict__ w, uint64_t rows,
-                                           uint64_t cols, const Prologue &pro,
-                                           float *__restrict__ y, uint64_t half, uint32_t bid,
-                                           uint32_t nblocks, const Gate &gate,
-                                           const Signal &sig) {
+__global__ __launch_bounds__(kThreads) void gemv_regp_kernel(const uint16_t *__restrict__ w,
+                                                             uint64_t rows, uint64_t cols,
+                                                             Prologue pro, float *__restrict__ y,
+                                                             uint64_t half) {
     static_assert(!SWIGLU || U == 2, "a SwiGLU step is one gate/up row pair");
     // WPR waves share a step, each holding KC of the row's KC * WPR chunks;
     // their sums meet in LDS.
@@ -727,7 +621,7 @@ __device__ __forceinline__ void regp_block(const uint16_t *__restrict__ w, uint6
     extern __shared__ float xs[];
     __shared__ float red[4];
     __shared__ float part[4][U];
-    const bool through = sig.counter != nullptr;
+    const uint32_t bid = blockIdx.x, nblocks = gridDim.x;
     const uint32_t n = (uint32_t)cols;
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const uint32_t pidx = wave % WPR, grp = wave / WPR;
@@ -740,7 +634,7 @@ __device__ __forceinline__ void regp_block(const uint16_t *__restrict__ w, uint6
     const uint32_t u0 = ubase + grp;
     ProloguePart pp;
     prologue_begin(pro, n, pp);
-    if (!gate.counter) prologue_load(pro, pp);
+    prologue_load(pro, pp);
     __builtin_amdgcn_sched_barrier(0);
     u32x4 wv[U][KC];
     const uint32_t last = (uint32_t)rows - 1, uhalf = (uint32_t)half;
@@ -756,12 +650,8 @@ __device__ __forceinline__ void regp_block(const uint16_t *__restrict__ w, uint6
     };
     if (u0 < units) load(u0);
     __builtin_amdgcn_sched_barrier(0);
-    bool ok = true;
-    if (gate.counter) {
-        ok = gate_wait(gate);
-        prologue_load(pro, pp);
-    }
-    prologue_finish(pro, n, pp, xs, red, bid, through);
+    prologue_finish(pro, n, pp, xs, red, bid);
+    publish_status(pro, bid);
     float x[KC][8];
 #pragma unroll
     for (int c = 0; c < KC; ++c) {
@@ -788,7 +678,7 @@ __device__ __forceinline__ void regp_block(const uint16_t *__restrict__ w, uint6
                     a = __builtin_fmaf(__uint_as_float(q[e] & 0xffff0000u), x[c][2 * e + 1], a);
                 }
             }
-            acc[u] = ok ? wave_sum(a) : __builtin_nanf("");
+            acc[u] = wave_sum(a);
         }
         if (WPR > 1) {
             if (lane == 0)
@@ -807,24 +697,14 @@ __device__ __forceinline__ void regp_block(const uint16_t *__restrict__ w, uint6
         if (lane == 0 && pidx == 0 && valid) {
             if (SWIGLU) {
                 const float d = plamo_exp(-acc[0]) + 1.0f;
-                put(y + unit, (acc[0] / d) * acc[1], through);
+                y[unit] = (acc[0] / d) * acc[1];
             } else {
 #pragma unroll
                 for (int u = 0; u < U; ++u)
-                    if (unit * U + u < rows) put(y + unit * U + u, acc[u], through);
+                    if (unit * U + u < rows) y[unit * U + u] = acc[u];
             }
         }
     }
-    signal_done(sig, bid);
-}
-
-template <int KC, int U, bool SWIGLU, int WPR = 1>
-__global__ __launch_bounds__(kThreads) void gemv_regp_kernel(const uint16_t *__restrict__ w,
-                                                             uint64_t rows, uint64_t cols,
-                                                             Prologue pro, float *__restrict__ y,
-                                                             uint64_t half) {
-    regp_block<KC, U, SWIGLU, WPR>(w, rows, cols, pro, y, half, blockIdx.x, gridDim.x, Gate{},
-                                   Signal{});
 }
 
 // Column counts the register GEMV covers: cols = 512 * KC * WPR.
@@ -2163,8 +2043,7 @@ constexpr uint32_t kRowsPerBlock = 64;
 // and counts the head in *done (the fused O projection waits on it).
 template <int DIM, int G, int W>
 __device__ __forceinline__ void attention_block(const DecodeAttention &a, uint32_t kvh,
-                                                uint32_t split, uint32_t *done,
-                                                const Gate &gate) {
+                                                uint32_t split, uint32_t *done) {
     constexpr uint32_t RW = kRowsPerBlock / W;  // rows per wave
     constexpr uint32_t P = W * RW;              // rows per pass (one block)
     constexpr int HPW = (G + W - 1) / W;        // query heads per wave
@@ -2187,10 +2066,8 @@ __device__ __forceinline__ void attention_block(const DecodeAttention &a, uint32
     // The step's query/key/value heads: wave w normalizes query heads w,
     // w + W, ..., the last wave the new key; lane j < DIM/2 holds elements j
     // and j + DIM/2. Loaded unconditionally (lanes and waves with no use read
-    // valid data they ignore) and kept as raw bits until used. Without a gate
-    // they go out first (they do not depend on the row count); with a gate
-    // (they are produced by an earlier phase of the launch) after the cached
-    // K/V rows, which do not depend on them.
+    // valid data they ignore) and kept as raw bits until used. They go out
+    // first: they do not depend on the row count.
     const bool kwave = wave == W - 1;
     const bool hl = lane < HALF;
     const uint32_t hj = lane % HALF;
@@ -2215,7 +2092,7 @@ __device__ __forceinline__ void attention_block(const DecodeAttention &a, uint32
         vx[0] = vsrc[hj];
         vx[1] = vsrc[hj + HALF];
     };
-    if (!gate.counter) load_inputs();
+    load_inputs();
     const float freq = a.freq[hj];
 
     const uint32_t count = a.params->count[a.layer];
@@ -2276,11 +2153,6 @@ __device__ __forceinline__ void attention_block(const DecodeAttention &a, uint32
     const uint32_t hr = hi < count ? hi : count;  // cached rows of this block
     float rc, rs;
     rope_cos_sin(freq, a.rope_scale, (float)count, rc, rs);
-    bool ok = true;
-    if (gate.counter) {
-        ok = gate_wait(gate);
-        load_inputs();
-    }
 
     // Offset-1 head RMSNorm then split-half rotation (src/qkv.s:36-67,
     // tests/rope_reference.s:14-30).
@@ -2489,7 +2361,7 @@ __device__ __forceinline__ void attention_block(const DecodeAttention &a, uint32
 #pragma unroll
         for (uint32_t w = 0; w < (uint32_t)W; ++w) o = o + wpart[(w * G + g) * DIM + d];
         if (splits == 1) {
-            const float r = ok ? o / stats[g][1] : __builtin_nanf("");
+            const float r = o / stats[g][1];
             if (done)
                 store_through(a.out + (uint64_t)(kvh * G + g) * DIM + d, r);
             else
@@ -2497,7 +2369,7 @@ __device__ __forceinline__ void attention_block(const DecodeAttention &a, uint32
         } else {
             float *bp = a.partial + ((uint64_t)(kvh * a.splits + split) * G + g) * rec;
             if (d == 0) {
-                store_through(bp, ok ? stats[g][0] : __builtin_nanf(""));
+                store_through(bp, stats[g][0]);
                 store_through(bp + 1, stats[g][1]);
             }
             store_through(bp + 2 + d, o);
@@ -2556,7 +2428,7 @@ __device__ __forceinline__ void attention_block(const DecodeAttention &a, uint32
 
 template <int DIM, int G>
 __global__ __launch_bounds__(kAttnThreads) void decode_attention_kernel(DecodeAttention a) {
-    attention_block<DIM, G, kAttnWaves>(a, blockIdx.x, blockIdx.y, nullptr, Gate{});
+    attention_block<DIM, G, kAttnWaves>(a, blockIdx.x, blockIdx.y, nullptr);
 }
 
 // Attention fused with the output projection (src/mixer.s:60-80: O = W_o .
@@ -2591,11 +2463,16 @@ __device__ __forceinline__ void oproj_block(const AttentionO &f, uint32_t ob) {
 #pragma unroll
         for (int c = 0; c < KC; ++c) wv[u][c] = __builtin_nontemporal_load(p + c * 64);
     }
+    // Zero in the step's parameters means: wait for every KV head, up to
+    // 2^22 polls. Other values exist for tests, which raise the target past
+    // the heads so that the wait gives up while every block still exits.
+    const uint32_t target = f.heads + f.a.params->wait_extra;
+    const uint32_t limit = f.a.params->wait_limit ? f.a.params->wait_limit : (1u << 22);
     uint32_t spins = 0;
     bool ok = true;
-    while (__hip_atomic_load(f.done, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < f.heads) {
+    while (__hip_atomic_load(f.done, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
         __builtin_amdgcn_s_sleep(2);
-        if (++spins == (1u << 22)) {
+        if (++spins >= limit) {
             ok = false;
             break;
         }
@@ -2630,8 +2507,7 @@ template <int DIM, int G, int KC>
 __global__ __launch_bounds__(kAttnThreads) void attention_o_kernel(AttentionO f) {
     const uint32_t attention_blocks = f.a.kh * f.a.splits;
     if (blockIdx.x < attention_blocks)
-        attention_block<DIM, G, kAttnWaves>(f.a, blockIdx.x % f.a.kh, blockIdx.x / f.a.kh, f.done,
-                                            Gate{});
+        attention_block<DIM, G, kAttnWaves>(f.a, blockIdx.x % f.a.kh, blockIdx.x / f.a.kh, f.done);
     else
         oproj_block<KC>(f, blockIdx.x - attention_blocks);
 }
@@ -2722,126 +2598,6 @@ hipError_t launch_decode_attention(hipStream_t stream, const DecodeAttention &a)
     if (!decode_attention_supported(a.dim, a.qh / a.kh) || a.splits < 1 || a.splits > 65535)
         return hipErrorInvalidValue;
     return a.dim == 64 ? decode_attention_dim<64>(stream, a) : decode_attention_dim<128>(stream, a);
-}
-
-// ---------------------------------------------------------------- fused layer
-// One decoder layer of a decode step (src/forward.s layer loop: src/mixer.s
-// QKV, attention and O; src/mlp.s gate/up, SwiGLU and down) as one launch.
-// Blocks are ordered by phase: [QKV | attention | O | gate/up | down]. A
-// block of a later phase first requests its weights, then waits until every
-// block of the phase it reads has counted itself, so one phase's tail
-// overlaps the next phase's weight stream instead of a launch boundary
-// draining the GPU between them. Every wait is on lower-numbered blocks,
-// which are dispatched first, so it ends; it is also bounded (a block that
-// gives up writes NaN and sets the error flag).
-// Coherence: whatever a phase reads from an earlier phase of the launch (the
-// QKV output, the attention output, the O output, the residual state, the
-// SwiGLU output) is read by no block before its wait, so no cache holds a
-// stale copy; producers write it through to the coherence point and wait
-// for the stores before counting themselves.
-constexpr int kLayerAttnWaves = (int)(kThreads / 64);
-
-template <int DIM, int G, int OKC, int OWPR, int OU, int DKC, int DWPR, int DU>
-__global__ __launch_bounds__(kThreads) void layer_kernel(LayerStep l) {
-    uint32_t b = blockIdx.x;
-    const uint32_t na = l.a.kh * l.a.splits;
-    if (b < l.nq) {
-        gemv_block<true, false>(l.qkv_w, l.qkv_rows, l.hidden, l.pq, l.qkv, 0, b, l.nq, Gate{},
-                                Signal{l.phase, kPhaseLanes});
-        return;
-    }
-    b -= l.nq;
-    if (b < na) {
-        attention_block<DIM, G, kLayerAttnWaves>(l.a, b % l.a.kh, b / l.a.kh, l.phase + kPhaseWords,
-                                                 Gate{l.phase, kPhaseLanes, l.nq, l.error});
-        return;
-    }
-    b -= na;
-    if (b < l.no) {
-        reg_block<OKC, OWPR, OU>(l.o_w, l.hidden, (uint64_t)l.a.qh * DIM, l.a.out, l.branch, b,
-                                 l.no, Gate{l.phase + kPhaseWords, 1, l.a.kh, l.error},
-                                 Signal{l.phase + 2 * kPhaseWords, kPhaseLanes});
-        return;
-    }
-    b -= l.no;
-    if (b < l.ng) {
-        gemv_block<true, true>(l.gu_w, 2ull * l.inter, l.hidden, l.pg, l.act, l.inter, b, l.ng,
-                               Gate{l.phase + 2 * kPhaseWords, kPhaseLanes, l.no, l.error},
-                               Signal{l.phase + 3 * kPhaseWords, kPhaseLanes});
-        return;
-    }
-    b -= l.ng;
-    if (b < l.nd)
-        reg_block<DKC, DWPR, DU>(l.down_w, l.hidden, l.inter, l.act, l.down_out, b, l.nd,
-                                 Gate{l.phase + 3 * kPhaseWords, kPhaseLanes, l.ng, l.error},
-                                 Signal{});
-}
-
-// Shapes with a fused variant: the register GEMV configuration of the O and
-// down projections is the one the separate launches use for those widths.
-enum LayerVariant { kLayerNone, kLayerG4O2048D8192, kLayerG4O2048D10240, kLayerG4O4096D16384,
-                    kLayerG6O6144D24576 };
-
-static LayerVariant layer_variant(const LayerStep &l) {
-    if (l.a.dim != 128 || !l.a.kh || l.a.qh % l.a.kh) return kLayerNone;
-    const uint32_t g = l.a.qh / l.a.kh, ocols = l.a.qh * l.a.dim;
-    if (g == 4 && ocols == 2048 && l.inter == 8192) return kLayerG4O2048D8192;
-    if (g == 4 && ocols == 2048 && l.inter == 10240) return kLayerG4O2048D10240;
-    if (g == 4 && ocols == 4096 && l.inter == 16384) return kLayerG4O4096D16384;
-    if (g == 6 && ocols == 6144 && l.inter == 24576) return kLayerG6O6144D24576;
-    return kLayerNone;
-}
-
-template <int DIM, int G, int OKC, int OWPR, int OU, int DKC, int DWPR, int DU>
-static void layer_counts(LayerStep &l, uint32_t hint) {
-    auto cap = [&](uint64_t n) { return (uint32_t)(n < hint ? (n ? n : 1) : hint); };
-    l.nq = cap((((uint64_t)l.qkv_rows + 1) / 2 + 3) / 4);
-    l.no = cap((((uint64_t)l.hidden + OU - 1) / OU + (4 / OWPR) - 1) / (4 / OWPR));
-    l.ng = cap(((uint64_t)l.inter + 3) / 4);
-    l.nd = cap((((uint64_t)l.hidden + DU - 1) / DU + (4 / DWPR) - 1) / (4 / DWPR));
-}
-
-template <int DIM, int G, int OKC, int OWPR, int OU, int DKC, int DWPR, int DU>
-static hipError_t layer_launch(hipStream_t stream, const LayerStep &l) {
-    const void *k = (const void *)layer_kernel<DIM, G, OKC, OWPR, OU, DKC, DWPR, DU>;
-    size_t lds = std::max<size_t>((size_t)l.hidden * sizeof(float),
-                                  decode_attention_lds(DIM, G, kLayerAttnWaves));
-    if (lds > 65536) {
-        hipError_t e = hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-        if (e != hipSuccess) return e;
-    }
-    const uint64_t grid = (uint64_t)l.nq + (uint64_t)l.a.kh * l.a.splits + l.no + l.ng + l.nd;
-    layer_kernel<DIM, G, OKC, OWPR, OU, DKC, DWPR, DU>
-        <<<(unsigned)grid, kThreads, lds, stream>>>(l);
-    return hipGetLastError();
-}
-
-bool layer_plan(LayerStep &l, uint32_t blocks_hint) {
-    // The fused variant's GEMVs are the vector forms: 16-byte aligned weight
-    // rows and inputs, widths in whole 512-column chunks where registers hold x.
-    const uintptr_t align = (uintptr_t)l.qkv_w | (uintptr_t)l.o_w | (uintptr_t)l.gu_w |
-                            (uintptr_t)l.down_w | (uintptr_t)l.a.out | (uintptr_t)l.act;
-    if ((align & 15) || l.hidden % 8 || !blocks_hint || !l.phase || !l.error) return false;
-    if (!l.a.splits || l.a.splits > 65535) return false;
-    if (l.qkv_rows != (l.a.qh + 2 * l.a.kh) * l.a.dim) return false;
-    switch (layer_variant(l)) {
-    case kLayerG4O2048D8192: layer_counts<128, 4, 4, 1, 2, 8, 2, 1>(l, blocks_hint); return true;
-    case kLayerG4O2048D10240: layer_counts<128, 4, 4, 1, 2, 5, 4, 1>(l, blocks_hint); return true;
-    case kLayerG4O4096D16384: layer_counts<128, 4, 8, 1, 2, 8, 4, 1>(l, blocks_hint); return true;
-    case kLayerG6O6144D24576: layer_counts<128, 6, 6, 2, 2, 12, 4, 1>(l, blocks_hint); return true;
-    default: return false;
-    }
-}
-
-hipError_t launch_layer(hipStream_t stream, const LayerStep &l) {
-    if (!l.nq || !l.no || !l.ng || !l.nd || !l.phase || !l.error) return hipErrorInvalidValue;
-    switch (layer_variant(l)) {
-    case kLayerG4O2048D8192: return layer_launch<128, 4, 4, 1, 2, 8, 2, 1>(stream, l);
-    case kLayerG4O2048D10240: return layer_launch<128, 4, 4, 1, 2, 5, 4, 1>(stream, l);
-    case kLayerG4O4096D16384: return layer_launch<128, 4, 8, 1, 2, 8, 4, 1>(stream, l);
-    case kLayerG6O6144D24576: return layer_launch<128, 6, 6, 2, 2, 12, 4, 1>(stream, l);
-    default: return hipErrorInvalidValue;
-    }
 }
 
 // ---------------------------------------------------------------- prompt attention

@@ -203,14 +203,14 @@ EXPORTS = {
                         "plamo_metal_prepare_model", "plamo_metal_forward",
                         "plamo_metal_prefill", "plamo_metal_verify", "plamo_metal_commit",
                         "plamo_metal_linear", "plamo_metal_mlp"],
-    "plamo_diag.h": ["plamo_hip_time_kernel"],
+    "plamo_diag.h": ["plamo_hip_time_kernel", "plamo_hip_debug_waits"],
     "plamo_draft.h": ["plamo_draft_open", "plamo_draft_close", "plamo_draft_reset",
                       "plamo_draft_propose", "plamo_draft_accept", "plamo_draft_checkpoint",
                       "plamo_draft_restore", "plamo_draft_checkpoint_free",
                       "plamo_hip_draft_open", "plamo_hip_draft_install",
                       "plamo_hip_draft_set_tokenizer", "plamo_hip_draft_reset_ids",
                       "plamo_hip_draft_get_stats", "plamo_hip_draft_next_horizon",
-                      "plamo_hip_decode", "plamo_hip_rewind"],
+                      "plamo_hip_decode", "plamo_hip_rewind", "plamo_hip_invalidate"],
     "plamo_synthetic.h": ["plamo_synthetic_defaults", "plamo_synthetic_build",
                           "plamo_synthetic_free", "plamo_synthetic_weights",
                           "plamo_synthetic_frequencies", "plamo_synthetic_instantiate",
@@ -272,6 +272,8 @@ def load() -> ctypes.CDLL:
                                      c_uint, c_uint, TOKEN_FN, c_void_p, POINTER(DecodeResult),
                                      c_char_p, c_size_t]),
         "plamo_hip_rewind": (c_int, [c_void_p, M, c_uint64]),
+        "plamo_hip_invalidate": (None, [c_void_p]),
+        "plamo_hip_debug_waits": (None, [c_void_p, c_uint32, c_uint32]),
         "plamo_synthetic_defaults": (None, [POINTER(SyntheticConfig)] + [c_uint64] * 7),
         "plamo_synthetic_build": (c_void_p, [POINTER(SyntheticConfig), c_uint, c_char_p,
                                              c_size_t]),
@@ -546,6 +548,15 @@ class Backend:
     def maintain(self):
         """Waits for the backend's stream (runtime/metal.h:51)."""
         self.lib.plamo_metal_maintain(self.handle)
+
+    def invalidate(self):
+        """Every layer's host rows are uploaded by the next call."""
+        self.lib.plamo_hip_invalidate(self.handle)
+
+    def debug_waits(self, extra: int, polls: int):
+        """Test hook: the decode attention's O blocks wait for `extra` more KV
+        heads than exist, giving up after `polls` polls (0, 0: normal)."""
+        self.lib.plamo_hip_debug_waits(self.handle, extra, polls)
 
     def time_kernel(self, inst: Instance, layer: int, which: int, reps: int):
         """(ms per launch, algorithmic bytes per launch) of one decode kernel."""

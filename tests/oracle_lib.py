@@ -39,6 +39,7 @@ def load():
         "oracle_swiglu": (None, [f32p, f32p, c_uint64]),
         "oracle_matvec": (None, [u16p, f32p, f32p, c_uint64, c_uint64]),
         "oracle_matmul": (None, [POINTER(plamo_hip.Matmul)]),
+        "oracle_matmul_blocked": (None, [POINTER(plamo_hip.Matmul)]),
         "oracle_set_threads": (None, [c_uint]),
         "oracle_threads": (c_uint, []),
         "oracle_rmsnorm": (None, [f32p, u16p, f32p, c_uint64, c_float, c_float]),

@@ -69,10 +69,12 @@ def test_decode_steps(h, inter, dim, capacity, pinned):
         s.close()
 
 
-PROMPTS = [1, 2, 3, 4, 7, 8, 9, 17, 31, 32, 33, 116, 128, 129, 255, 257]
+# tests/metal_decode.c:239-240 (4096 only after a 2-token prefix, :249-250).
+PROMPTS = [1, 2, 3, 4, 7, 8, 9, 17, 31, 32, 33, 116, 128, 129, 255, 256, 257, 443, 511, 512, 513,
+           4096]
 
 
-@pytest.mark.parametrize("h,inter,dim,capacity", [(7, 11, 6, 600), (128, 257, 128, 300)])
+@pytest.mark.parametrize("h,inter,dim,capacity", [(7, 11, 6, 4100), (128, 257, 128, 600)])
 def test_prefill_then_decode(h, inter, dim, capacity):
     s = tiny(h=h, inter=inter, dim=dim, capacity=capacity)
     a, b = s.instance(), s.instance()
@@ -80,7 +82,7 @@ def test_prefill_then_decode(h, inter, dim, capacity):
     try:
         for prefix in (0, 2, 6):
             for n in PROMPTS:
-                if n + prefix >= capacity:
+                if n + prefix >= capacity or (n == 4096 and prefix != 2):
                     continue
                 for final_only in (0, 1):
                     say(f"prefill h={h} prefix={prefix} n={n} final_only={final_only}")
@@ -224,6 +226,18 @@ def test_host_edits_are_uploaded():
             assert oracle_lib.forward(a, 5) and oracle_lib.forward(b, 5)
             assert be.forward(a, 6) == 1 and oracle_lib.forward(b, 6)
             compare(a, b)
+            # An edit of the last V row alone (counts and K rows unchanged).
+            for inst in (a, b):
+                i = 1
+                inst.kv(i, "v")[inst.cache(i).count - 1] *= 0.5
+            assert be.forward(a, 2) == 1 and oracle_lib.forward(b, 2)
+            compare(a, b)
+            # An edit of an earlier row at unchanged counters: announced.
+            for inst in (a, b):
+                inst.kv(1, "v")[0] += 1.0
+            be.invalidate()
+            assert be.forward(a, 4) == 1 and oracle_lib.forward(b, 4)
+            compare(a, b)
             # Draft-style restore: rows kept, rotations marked stale.
             for inst in (a, b):
                 for i in range(2):
@@ -317,6 +331,42 @@ def test_decline_and_failure_contract():
         be.close()
     finally:
         a.close()
+        s.close()
+
+
+@pytest.mark.parametrize("pinned", [False, True])
+def test_device_wait_failure_is_reported(pinned):
+    # runtime/metal.h:63-67: a step that fails after partial writes returns -1
+    # (not retried) and counts an error. The host raises the target of the
+    # decode attention's bounded wait past the KV heads and shortens it, so the
+    # output-projection blocks give up and every kernel still exits.
+    say(f"bounded wait gives up, pinned={pinned}")
+    s = plamo_hip.Synthetic(512, 2, 16, 4, 128, 1024, 300, window=8, global_capacity=64,
+                            pattern=2, seed=21)  # attention width 2048: the fused kernel
+    a, b = s.instance(pinned=pinned), s.instance()
+    be = plamo_hip.Backend(s)
+    try:
+        assert be.prefill(a, [3, 9, 27]) == 1 and oracle_lib.prefill(b, [3, 9, 27])
+        assert be.forward(a, 5) == 1 and oracle_lib.forward(b, 5)
+        compare(a, b)
+        clean(be)
+        be.debug_waits(1, 256)
+        assert be.forward(a, 6) == -1
+        info = be.info()
+        assert info.errors == 1 and b"wait" in info.note
+        be.debug_waits(0, 0)
+        # The request is abandoned; the next one starts from a reset model.
+        a.reset()
+        b.reset()
+        assert be.prefill(a, [4, 8]) == 1 and oracle_lib.prefill(b, [4, 8])
+        for t in (6, 1):
+            assert be.forward(a, t) == 1 and oracle_lib.forward(b, t)
+            compare(a, b)
+        assert be.info().errors == 1
+    finally:
+        be.close()
+        a.close()
+        b.close()
         s.close()
 
 

@@ -1,19 +1,31 @@
-"""GPU parity at the BASELINE.json shapes (the production fast paths).
+"""GPU parity at the BASELINE.json shapes, on the default decode path (the
+captured graph of the bench) and the prompt/verify paths.
 
 C1: one layer, hidden 2048, 16/4 heads of 128, MLP 8192, KV
 pre-filled with 512 (then 254) rows of raw K/V ~ N(0,1) (rotations rebuilt by
 the first step on both sides); then decode steps and a prompt.
-C4 shapes with 4 of its 32 layers and a small vocabulary:
-covers the 16K-column down projection and the fused attention at group 4.
 C2 in full: 16 layers, vocab 100000, a 32-token prompt and 64
 greedy steps; the greedy ids must match the oracle's except after a step whose
 oracle top-2 logit gap is below 1e-3, and every
 step's logits pass the reference gate.
+C3 shapes with 2 of its 24 layers (one local, one global YaRN
+layer): attention width 2048 under hidden 2560, the 10240-column down
+projection; the engine's flow of a 12-token prefix restored from the prompt
+cache, then the 116- and 443-token suffixes of the 128- and 455-token prompts,
+then decode steps.
+C4 shapes with 4 of its 32 layers and the full 100000-token
+head: the 16K-column down projection and the fused attention at group 4.
+C5 shapes with 2 of its 60 layers and the tied head: six query
+heads per KV head, O and down at 6144 and 24576 columns; decode over a
+455-row prefix, then verify of 1-5 candidates (the token GEMV) and 6-16
+(the skinny GEMM) committed against sequential oracle forwards
+(tests/metal_decode.c:309-365 at this width).
 """
 
 import numpy as np
 import pytest
 
+import prompt_cache
 from parity import compare, gate, oracle_lib, plamo_hip, say
 
 pytestmark = pytest.mark.gpu
@@ -63,15 +75,13 @@ def test_c1_single_layer_prefilled_kv():
         syn.close()
 
 
-@pytest.mark.parametrize("layer_launch", ["1", "0"])
-def test_c4_shapes_four_layers(monkeypatch, layer_launch):
+def test_c4_shapes_four_layers():
     # Pinned host arrays: the decode graph writes logits, state, normalized
-    # state and the new K/V rows into them in place (the bench's setup).
-    # layer_launch 1: each decoder layer is one launch with phase-chained
-    # blocks; 0: one launch per projection and the attention.
-    monkeypatch.setenv("PLAMO_HIP_LAYER_LAUNCH", layer_launch)
-    say(f"c4 four layers, layer launch {layer_launch}")
-    cfg = dict(plamo_hip.CONFIGS["c4"], layers=4, vocab=1000)
+    # state and the new K/V rows into them in place (the bench's setup). The
+    # 100000-row head of the headline config, then pageable host arrays (the
+    # graph stages the step's outputs in a device outbox).
+    say("c4 four layers, vocab 100000")
+    cfg = dict(plamo_hip.CONFIGS["c4"], layers=4)
     syn = plamo_hip.Synthetic(**cfg, pattern=4, seed=202)
     try:
         run_pair(syn, steps=4, prompt=list(range(5, 5 + 69 * 7, 7)), pinned=True)
@@ -80,19 +90,109 @@ def test_c4_shapes_four_layers(monkeypatch, layer_launch):
         syn.close()
 
 
-@pytest.mark.parametrize("name", ["c3", "c5"])
-def test_layer_launch_variants(monkeypatch, name):
-    # The remaining one-launch layer shapes: C3 (hidden 2560, down 10240
-    # columns) and C5 (hidden 6144, six query heads per KV head, O 6144 and
-    # down 24576 columns), two layers each, with prefilled KV rows so the
-    # attention spans several blocks per KV head.
-    monkeypatch.setenv("PLAMO_HIP_LAYER_LAUNCH", "1")
-    cfg = dict(plamo_hip.CONFIGS[name], layers=2, vocab=500)
-    say(f"{name} two layers")
-    syn = plamo_hip.Synthetic(**cfg, embedding_std=1.0, seed=505)
+def test_c3_prefix_restore_and_prompts():
+    # runtime/engine.c:358-381: the 12-token template prefix is prefilled once
+    # and captured (runtime/prompt_cache.c); each request resets the model,
+    # restores the prefix rows and prefills the rest of its prompt. The oracle
+    # prefills the whole prompt from a reset model.
+    cfg = dict(plamo_hip.CONFIGS["c3"], layers=2, vocab=1000)
+    syn = plamo_hip.Synthetic(**cfg, pattern=2, seed=606)
+    gpu, cpu = syn.instance(pinned=True), syn.instance()
+    be = plamo_hip.Backend(syn)
     try:
-        run_pair(syn, steps=3, prompt=None, fill=300, pinned=True)
+        rng = np.random.default_rng(128)
+        prefix = rng.integers(0, cfg["vocab"], size=12).tolist()
+        assert be.prefill(gpu, prefix) == 1
+        snap = prompt_cache.capture(gpu, prefix)
+        assert snap is not None
+        for total in (128, 455):
+            say(f"c3 prompt {total} ({total - 12} after the restored prefix)")
+            ids = prefix + rng.integers(0, cfg["vocab"], size=total - 12).tolist()
+            gpu.reset()
+            cpu.reset()
+            assert prompt_cache.restore(snap, gpu, ids) == 12
+            assert be.prefill(gpu, ids[12:]) == 1
+            assert oracle_lib.prefill(cpu, ids)
+            compare(gpu, cpu)
+            token = prompt_cache.greedy(cpu)
+            for step in range(3):
+                assert be.forward(gpu, token) == 1
+                assert oracle_lib.forward(cpu, token)
+                compare(gpu, cpu)
+                token = prompt_cache.greedy(cpu)
+        info = be.info()
+        assert info.errors == 0 and info.cpu_fallbacks == 0, info.note.decode()
     finally:
+        be.close()
+        gpu.close()
+        cpu.close()
+        syn.close()
+
+
+def test_c5_decode_and_verify_over_455_rows():
+    cfg = dict(plamo_hip.CONFIGS["c5"], layers=2, vocab=500)
+    syn = plamo_hip.Synthetic(**cfg, pattern=2, embedding_std=1.0, seed=707)
+    gpu, cpu = syn.instance(pinned=True), syn.instance()
+    be = plamo_hip.Backend(syn)
+    try:
+        # 455 prefix rows of raw K/V ~ N(0,1); the first step rebuilds the
+        # rotations (eager), the next ones run the captured graph.
+        gpu.fill_kv(455, 9)
+        cpu.fill_kv(455, 9)
+        token = 7
+        for step in range(3):
+            say(f"c5 decode step {step}")
+            assert be.forward(gpu, token) == 1
+            assert oracle_lib.forward(cpu, token)
+            compare(gpu, cpu)
+            token = prompt_cache.greedy(cpu)
+        base = cpu.snapshot()
+        ids = [(i * 37 + 11) % cfg["vocab"] for i in range(16)]
+        for count in (1, 2, 3, 4, 5, 6, 8, 16):
+            say(f"c5 verify {count} candidates over {base['layers'][0][3]} rows")
+            cpu.restore(base)
+            states, logits, gold = [], [], []
+            for i in range(count):
+                assert oracle_lib.forward(cpu, ids[i])
+                states.append(cpu.state().copy())
+                logits.append(cpu.logits().copy())
+                gold.append(int(np.argmax(cpu.logits())))
+            # The oracle's rows replace the GPU's at unchanged counters: an
+            # edit the backend is told about (include/plamo_draft.h).
+            gpu.restore(base)
+            be.invalidate()
+            r, nxt = be.verify(gpu, ids[:count])
+            assert r == 1
+            for i in range(count):
+                top2 = np.sort(logits[i])[-2:]
+                if top2[1] - top2[0] >= 1e-3:
+                    assert nxt[i] == gold[i], f"candidate {i}"
+                assert be.commit(gpu, i) == 1
+                gate(gpu.state().copy(), states[i], f"verified state {i}")
+                gate(gpu.logits().copy(), logits[i], f"verified logits {i}")
+            compare(gpu, cpu)
+            assert be.commit(gpu, count) == 0
+            if count == 5:
+                # A rejected suffix: three commits, then an ordinary step.
+                cpu.restore(base)
+                for i in range(3):
+                    assert oracle_lib.forward(cpu, ids[i])
+                assert oracle_lib.forward(cpu, 12)
+                gpu.restore(base)
+                be.invalidate()
+                assert be.verify(gpu, ids[:count])[0] == 1
+                for i in range(3):
+                    assert be.commit(gpu, i) == 1
+                assert be.forward(gpu, 12) == 1
+                assert be.commit(gpu, 3) == 0
+                compare(gpu, cpu)
+        info = be.info()
+        assert info.errors == 0 and info.cpu_fallbacks == 0, info.note.decode()
+        assert info.verification_batches >= 9
+    finally:
+        be.close()
+        gpu.close()
+        cpu.close()
         syn.close()
 
 
