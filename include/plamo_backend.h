@@ -114,6 +114,22 @@ int plamo_metal_commit(struct plamo_metal *, struct model *, uint64_t index);
 /* runtime/metal.h:82-85. Synchronous projection output[t] = W * input[t] for
  * every token t (strides in FP32 elements). 0 = not handled. */
 int plamo_metal_linear(struct plamo_metal *, const struct plamo_matmul *);
+/* No counterpart in the reference. The projection of plamo_metal_linear for
+ * callers that cannot allocate (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc): input and output are the caller's
+ * DEVICE buffers (FP32, strides in elements), the weights a host address made
+ * resident by the config mappings or plamo_metal_preload, and the GEMM's
+ * scratch (split-K partial tiles, arrival counters, BF16 planes of the input)
+ * a static device array of PLAMO_HIP_STATIC_SCRATCH_BYTES held by each GPU
+ * until the process ends. Nothing is allocated. Rejected (0, reason in
+ * info.note): tokens > 1 with 3 * round_up(tokens, 128) * columns * 2 bytes
+ * of planes above PLAMO_HIP_STATIC_PLANE_BYTES, weights not resident, or no
+ * static scratch on the device. Enqueued on the backend's stream; returns
+ * after completion with the same bits as plamo_metal_linear. Calls that
+ * overlap on one GPU (from any backend instance) share the array and race. */
+#define PLAMO_HIP_STATIC_PLANE_BYTES (32ull << 20)
+#define PLAMO_HIP_STATIC_SCRATCH_BYTES ((64ull << 10) + (64ull << 20) + PLAMO_HIP_STATIC_PLANE_BYTES)
+int plamo_hip_linear_static(struct plamo_metal *, const struct plamo_matmul *);
 /* runtime/metal.h:86-88. Complete MLP branch on states[tokens, hidden]. */
 int plamo_metal_mlp(struct plamo_metal *, const struct mlp *, float *states, uint64_t tokens);
 

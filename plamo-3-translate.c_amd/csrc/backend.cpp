@@ -144,6 +144,21 @@ struct plamo_metal {
     std::vector<void *> allocations;
 };
 
+// Scratch of plamo_hip_linear_static: [arrival counters | split-K partial
+// tiles | BF16 planes of the input]. The partial region has the size of the
+// allocating GEMM workspace, so both entry points choose the same tiling and
+// produce the same bits. In host code `scratch` names a host-side stand-in:
+// only its device address (static_scratch[device], taken once per device at
+// plamo_metal_open) is ever passed to the GPU.
+constexpr uint64_t kStaticCounterBytes = 64ull << 10;
+constexpr uint64_t kStaticPartialBytes = kGemmPartialFloats * sizeof(float);
+static_assert(kStaticCounterBytes >= kGemmCounters * sizeof(uint32_t), "counters fit");
+static_assert(kStaticCounterBytes + kStaticPartialBytes + PLAMO_HIP_STATIC_PLANE_BYTES ==
+                  PLAMO_HIP_STATIC_SCRATCH_BYTES, "scratch layout");
+static __device__ __align__(256) unsigned char scratch[PLAMO_HIP_STATIC_SCRATCH_BYTES];
+constexpr int kMaxDevices = 64;
+static void *static_scratch[kMaxDevices];
+
 namespace {
 
 int problem(plamo_metal *m, const char *format, ...) {
@@ -1014,6 +1029,14 @@ struct plamo_metal *plamo_metal_open(const struct plamo_metal_config *config, ch
         return nullptr;
     }
     m->cus = prop.multiProcessorCount;
+    // The device address of this GPU's static scratch (once per device).
+    if (m->device < kMaxDevices && !static_scratch[m->device]) {
+        void *ptr = nullptr;
+        if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) == hipSuccess && ptr)
+            static_scratch[m->device] = ptr;
+        else
+            (void)hipGetLastError();
+    }
     snprintf(m->info.device, sizeof m->info.device, "%s (%s, %d CUs)", prop.name,
              prop.gcnArchName, prop.multiProcessorCount);
     snprintf(m->info.precision, sizeof m->info.precision, "fp32");
@@ -1682,6 +1705,60 @@ int plamo_metal_linear(struct plamo_metal *m, const struct plamo_matmul *mm) {
         return problem(m, "projection failed");
     }
     ++m->info.dispatches;
+    return 1;
+}
+
+int plamo_hip_linear_static(struct plamo_metal *m, const struct plamo_matmul *mm) {
+    if (!m) return 0;
+    if (!mm || !mm->input || !mm->output || !mm->rows || !mm->columns || !mm->tokens ||
+        mm->input_stride < mm->columns || mm->output_stride < mm->rows)
+        return problem(m, "static linear: invalid projection");
+    const uint64_t T = mm->tokens, K = mm->columns, N = mm->rows;
+    const uint16_t *w = (const uint16_t *)resolve(m, mm->weights, N * K * 2);
+    if (!w) return problem(m, "static linear: weights not resident");
+    char *base = m->device < kMaxDevices ? (char *)static_scratch[m->device] : nullptr;
+    if (!base) return problem(m, "static linear: no static scratch on this device");
+    if (T > 1 && gemm_plane_elems(T, K) * 2 > PLAMO_HIP_STATIC_PLANE_BYTES)
+        return problem(m,
+                       "static linear: %llu tokens x %llu columns need %llu bytes of input "
+                       "planes, above the static scratch's %llu",
+                       (unsigned long long)T, (unsigned long long)K,
+                       (unsigned long long)(gemm_plane_elems(T, K) * 2),
+                       (unsigned long long)PLAMO_HIP_STATIC_PLANE_BYTES);
+    if (configure_gemv(K) != hipSuccess) {
+        (void)hipGetLastError();
+        return problem(m, "static linear: %llu columns exceed the LDS budget",
+                       (unsigned long long)K);
+    }
+    GemmWorkspace ws{};
+    ws.counter_base = (uint32_t *)base;
+    ws.counters = kGemmCounters;
+    ws.partial = (float *)(base + kStaticCounterBytes);
+    ws.partial_floats = kGemmPartialFloats;
+    ws.planes = (uint16_t *)(base + kStaticCounterBytes + kStaticPartialBytes);
+    ws.plane_elems = PLAMO_HIP_STATIC_PLANE_BYTES / 2;
+    ws.cus = (uint32_t)m->cus;
+    const float *x = (const float *)mm->input;
+    float *y = mm->output;
+    hipStream_t s = m->stream;
+    begin_timing(m);
+    // The previous call on this GPU may have ended without leaving the
+    // counters at zero (a failed launch): clear them first.
+    bool ok = launch_fill(s, ws.counter_base, kGemmCounters, 0) == hipSuccess;
+    if (ok && T == 1) {
+        Prologue p{};
+        p.src = x;
+        ok = launch_gemv(s, w, N, K, p, y, 0, 2 * m->cus) == hipSuccess;
+    } else if (ok) {
+        ok = launch_gemm(s, x, mm->input_stride, w, N, K, T, y, mm->output_stride, &ws) ==
+             hipSuccess;
+    }
+    ok = ok && end_timing(m);
+    if (!ok) {
+        (void)hipGetLastError();
+        return problem(m, "static linear: launch failed");
+    }
+    m->info.dispatches += 2;
     return 1;
 }
 

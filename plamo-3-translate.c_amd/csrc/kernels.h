@@ -204,6 +204,8 @@ struct CopyRow {
     uint64_t floats;
 };
 hipError_t launch_copy_rows(hipStream_t, const CopyRow *table, uint32_t entries);
+// p[0, words) = value (a kernel, so that it is also safe inside captured graphs).
+hipError_t launch_fill(hipStream_t, uint32_t *p, uint64_t words, uint32_t value);
 // Raises the dynamic LDS limit of the GEMV variants to hold `cols` floats.
 hipError_t configure_gemv(uint64_t max_cols);
 // First maximal index per row (strict >); any NaN gives 0xffffffff. scratch:

@@ -2928,6 +2928,20 @@ hipError_t launch_copy_rows(hipStream_t stream, const CopyRow *table, uint32_t e
     return hipGetLastError();
 }
 
+__global__ __launch_bounds__(kThreads) void fill_kernel(uint32_t *p, uint64_t words,
+                                                        uint32_t value) {
+    for (uint64_t i = (uint64_t)blockIdx.x * kThreads + threadIdx.x; i < words;
+         i += (uint64_t)gridDim.x * kThreads)
+        p[i] = value;
+}
+
+hipError_t launch_fill(hipStream_t stream, uint32_t *p, uint64_t words, uint32_t value) {
+    if (!words) return hipSuccess;
+    const uint64_t blocks = std::min<uint64_t>((words + kThreads - 1) / kThreads, 1024);
+    fill_kernel<<<(unsigned)blocks, kThreads, 0, stream>>>(p, words, value);
+    return hipGetLastError();
+}
+
 // ---------------------------------------------------------------- argmax
 // src/token.s:37-63: first maximal index; NaN anywhere gives 0xffffffff.
 // First maximal index of each row (strict >, ties to the lower index); a row

@@ -202,7 +202,7 @@ EXPORTS = {
                         "plamo_metal_get_info", "plamo_metal_preload", "plamo_metal_warm_cache",
                         "plamo_metal_prepare_model", "plamo_metal_forward",
                         "plamo_metal_prefill", "plamo_metal_verify", "plamo_metal_commit",
-                        "plamo_metal_linear", "plamo_metal_mlp"],
+                        "plamo_metal_linear", "plamo_metal_mlp", "plamo_hip_linear_static"],
     "plamo_diag.h": ["plamo_hip_time_kernel", "plamo_hip_debug_waits"],
     "plamo_draft.h": ["plamo_draft_open", "plamo_draft_close", "plamo_draft_reset",
                       "plamo_draft_propose", "plamo_draft_accept", "plamo_draft_checkpoint",
@@ -247,6 +247,7 @@ def load() -> ctypes.CDLL:
                                        POINTER(c_uint32)]),
         "plamo_metal_commit": (c_int, [c_void_p, M, c_uint64]),
         "plamo_metal_linear": (c_int, [c_void_p, POINTER(Matmul)]),
+        "plamo_hip_linear_static": (c_int, [c_void_p, POINTER(Matmul)]),
         "plamo_metal_mlp": (c_int, [c_void_p, POINTER(Mlp), f32p, c_uint64]),
         "plamo_forward": (c_int, [M, c_uint64]),
         "plamo_prefill": (c_int, [M, POINTER(c_uint32), c_uint64, f32p]),
