@@ -80,29 +80,107 @@ def prefill_flop(cfg: dict, prefix: int, tokens: int) -> float:
     return linear + attention
 
 
-def cpu_baseline(inst: plamo_hip.Instance, token: int, seconds: float, cfg: dict):
-    """Oracle decode steps on the host cores, continuing the GPU's sequence on
-    the same (coherent) host arrays."""
+def host_threads() -> tuple[int, int]:
+    """(threads the CPU baseline uses, nproc). The threads are this process's
+    CPU share: its affinity set, capped by OMP_NUM_THREADS when the host sets
+    it (a shared GPU box allots each GPU a slice of its cores)."""
+    nproc = os.cpu_count() or 1
+    share = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else nproc
+    cap = os.environ.get("OMP_NUM_THREADS", "")
+    if cap.isdigit() and int(cap) > 0:
+        share = min(share, int(cap))
+    return max(1, share), nproc
+
+
+def cpu_baseline(inst: plamo_hip.Instance, token: int, seconds: float, cfg: dict, prompt,
+                 snap) -> dict:
+    """The C oracle on the host cores, on bounded
+    samples of the same workloads: decode steps of the model continuing the
+    GPU's sequence on the same host arrays at N threads and at 1 thread, the
+    C1 layer step at both, and the 128-token prompt's prefill
+    (12-token prefix restored, 116 tokens) over the first layers of the model
+    at N threads and over its first layer at 1 thread, scaled to every layer.
+    Rows are split over threads in groups of 24 as runtime/parallel.c:35-48;
+    the prefill runs its projections token-blocked as the reference's prompt
+    path does (src/batch.s, src/matmul8x3.s)."""
     sys.path.insert(0, str(ROOT / "tests"))
     import oracle_lib  # the checker's CPU path; test infrastructure, not the product
 
     lib = oracle_lib.load()
-    threads = max(1, min(16, os.cpu_count() or 1))
-    lib.oracle_set_threads(threads)
-    steps, start = 0, time.perf_counter()
-    while True:
-        if not lib.oracle_forward(inst.model_ptr, token):
-            raise RuntimeError("oracle decode failed")
-        token = int(lib.oracle_argmax(inst.model.logits, inst.model.vocab))
-        steps += 1
-        elapsed = time.perf_counter() - start
-        if elapsed >= seconds or steps >= 64:
-            break
-    return {"value": steps / elapsed, "unit": "tok/s", "cores": threads, "kind": "port",
-            "sample": f"{steps} greedy decode steps of the {cfg['name']} model by the scalar C "
-                      f"oracle (gcc -O2 -ffp-contract=off, row-split over {threads} threads as "
-                      f"runtime/parallel.c:35-48), continuing the GPU run's sequence; "
-                      f"{elapsed:.1f} s"}
+    threads, nproc = host_threads()
+    model = inst.model_ptr
+
+    def decode(n_threads, budget, max_steps):
+        nonlocal token
+        lib.oracle_set_threads(n_threads)
+        steps, start = 0, time.perf_counter()
+        while True:
+            if not lib.oracle_forward(model, token):
+                raise RuntimeError("oracle decode failed")
+            token = int(lib.oracle_argmax(inst.model.logits, inst.model.vocab))
+            steps += 1
+            elapsed = time.perf_counter() - start
+            if elapsed >= budget or steps >= max_steps:
+                return steps, elapsed
+
+    steps_n, t_n = decode(threads, seconds * 0.3, 64)
+    steps_1, t_1 = decode(1, seconds * 0.2, 64)
+
+    # C1: one layer (hidden 2048, 16/4 heads of 128, MLP 8192), 512 rows of
+    # pre-filled KV; one decode step of the layer stack.
+    c1 = dict(plamo_hip.CONFIGS["c1"])
+    syn1 = plamo_hip.Synthetic(**c1, embedding_std=1.0, seed=101)
+    layer_ms = {}
+    try:
+        for n_threads in (threads, 1):
+            one = syn1.instance()
+            one.fill_kv(512, 7)
+            lib.oracle_set_threads(n_threads)
+            assert lib.oracle_forward(one.model_ptr, 3)  # rebuilds the rotations
+            times = []
+            for step in range(5):
+                start = time.perf_counter()
+                assert lib.oracle_forward(one.model_ptr, step % c1["vocab"])
+                times.append(time.perf_counter() - start)
+            layer_ms[str(n_threads)] = round(float(np.median(times)) * 1e3, 3)
+            one.close()
+    finally:
+        syn1.close()
+
+    # Prefill of the 116-token body over the first `layers` layers (a model
+    # descriptor with a shorter layer list over the same arrays), scaled.
+    def prefill(n_threads, layers):
+        restore(inst, snap, PREFIX)
+        view = plamo_hip.Model.from_buffer_copy(inst.model)
+        view.count = layers
+        ids = (ctypes.c_uint32 * (128 - PREFIX))(*prompt[PREFIX:128])
+        lib.oracle_set_threads(n_threads)
+        start = time.perf_counter()
+        if not lib.oracle_prefill(ctypes.byref(view), ids, 128 - PREFIX, None):
+            raise RuntimeError("oracle prefill failed")
+        return time.perf_counter() - start
+
+    L = cfg["layers"]
+    sample_n = min(L, 4)
+    p_n = prefill(threads, sample_n)
+    p_1 = prefill(1, 1)
+    return {"value": steps_n / t_n, "unit": "tok/s", "cores": threads, "kind": "port",
+            "nproc": nproc,
+            "one_thread_tok_s": steps_1 / t_1,
+            "c1_layer_step_ms": layer_ms,
+            "prefill_128_s": {str(threads): round(p_n * L / sample_n, 2),
+                              "1": round(p_1 * L, 2),
+                              "measured": f"{sample_n} of {L} layers at {threads} threads "
+                                          f"({p_n:.2f} s), 1 of {L} at 1 thread "
+                                          f"({p_1:.2f} s), scaled by layer count"},
+            "sample": f"{cfg['name']} decode: {steps_n} greedy steps at {threads} threads "
+                      f"({t_n:.1f} s) and {steps_1} at 1 thread ({t_1:.1f} s), continuing "
+                      f"the GPU run's sequence; C1 layer step: median of 5; prefill: the "
+                      f"116-token body of the 128-token prompt after the restored prefix. "
+                      f"Scalar C oracle (gcc -O2 -ffp-contract=off; prompt projections "
+                      f"token-blocked with AVX2 fused multiply-adds, same bits), rows split "
+                      f"over threads as runtime/parallel.c:35-48; {threads} threads = this "
+                      f"process's CPU share of the {nproc}-CPU host"}
 
 
 def copy_calibration(nbytes: int, reps: int = 5):
@@ -150,7 +228,7 @@ def verify_sweep(args) -> dict:
     through the matrix-core skinny GEMM."""
     tcfg = dict(plamo_hip.CONFIGS["c5"])
     tied = tcfg.pop("tied", 0)
-    threads = min(16, os.cpu_count() or 1)
+    threads = host_threads()[0]
     target = plamo_hip.Synthetic(**tcfg, tied=tied, seed=20261201, threads=threads)
     inst = target.instance(pinned=True)
     be = plamo_hip.Backend(target)
@@ -203,7 +281,7 @@ def speculative(args) -> dict:
     tcfg = dict(plamo_hip.CONFIGS["c5"])
     tied = tcfg.pop("tied", 0)
     dcfg = dict(plamo_hip.CONFIGS["c2"])
-    threads = min(16, os.cpu_count() or 1)
+    threads = host_threads()[0]
     t0 = time.perf_counter()
     target = plamo_hip.Synthetic(**tcfg, tied=tied, seed=20261201, threads=threads)
     source = plamo_hip.Synthetic(**dcfg, seed=20261202, threads=threads)
@@ -307,7 +385,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--config", default="c4", choices=sorted(plamo_hip.CONFIGS))
     ap.add_argument("--prompt", type=int, default=128)
-    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--ttft-sizes", default="81,128,455",
                     help="comma-separated prompt lengths for TTFT ('' skips)")
@@ -337,7 +415,7 @@ def main() -> int:
     tied = cfg.pop("tied", 0)
     shape = {k: cfg[k] for k in ("hidden", "layers", "qh", "kh", "dim", "intermediate", "vocab")}
     t0 = time.perf_counter()
-    syn = plamo_hip.Synthetic(**shape, tied=tied, seed=20261201, threads=min(16, os.cpu_count() or 1))
+    syn = plamo_hip.Synthetic(**shape, tied=tied, seed=20261201, threads=host_threads()[0])
     log(f"synthetic {args.config} weights: {syn.mapping.bytes / 1e9:.2f} GB in "
         f"{time.perf_counter() - t0:.1f} s")
     inst = syn.instance(pinned=True)
@@ -448,8 +526,11 @@ def main() -> int:
     }
     if not args.no_cpu:
         log("CPU baseline (oracle) ...")
-        result["cpu_baseline"] = cpu_baseline(inst, token, args.cpu_seconds, cfg)
-        log(f"CPU baseline: {result['cpu_baseline']['value']:.3f} tok/s")
+        result["cpu_baseline"] = cpu_baseline(inst, token, args.cpu_seconds, cfg, prompt, snap)
+        cb = result["cpu_baseline"]
+        log(f"CPU baseline: {cb['value']:.3f} tok/s at {cb['cores']} threads, "
+            f"{cb['one_thread_tok_s']:.3f} at 1; C1 layer {cb['c1_layer_step_ms']} ms; "
+            f"prefill 128 {cb['prefill_128_s']}")
     be.close()
     inst.close()
     syn.close()

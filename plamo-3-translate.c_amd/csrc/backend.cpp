@@ -71,7 +71,7 @@ struct Layer {
     float *host_k = nullptr, *host_v = nullptr, *host_rot = nullptr;  // device views of pinned host rows
     uint64_t rows = 0;          // device rows allocated
     // Shadow of the host bookkeeping after this backend's last return: the
-    // counters and the last K and V rows ([K row | V row]).
+    // counters and a sample of the last K and V rows ([K sample | V sample]).
     bool synced = false;
     uint64_t count = 0, processed = 0, scale_bits = 0;
     std::vector<float> last_kv;
@@ -110,6 +110,7 @@ struct plamo_metal {
     uint32_t max_splits = 1;   // attention blocks per KV head at full capacity
 
     StepParams *params_host = nullptr, *params_dev = nullptr;
+    StepParams *params_view = nullptr;  // device view of params_host (pinned)
     // Decode workspace.
     float *state_a = nullptr, *state_b = nullptr, *qkv = nullptr, *q = nullptr, *attn = nullptr,
           *branch = nullptr, *act = nullptr, *down_out = nullptr, *partial = nullptr;
@@ -235,6 +236,28 @@ uint32_t float_bits(float f) {
     uint32_t u;
     memcpy(&u, &f, 4);
     return u;
+}
+
+// The shadow's sample of a layer's last K and V rows: their first and last
+// kProbe values (the whole rows when narrower). A step writes these rows from
+// the device, so they are cold in the host's caches: sampling keeps the check
+// to a few cache lines per layer instead of whole rows.
+constexpr uint64_t kProbe = 16;
+uint64_t probe_floats(uint64_t width) { return width < 2 * kProbe ? width : 2 * kProbe; }
+
+void probe_row(const float *row, uint64_t width, float *out) {
+    if (width < 2 * kProbe) {
+        memcpy(out, row, width * 4);
+        return;
+    }
+    memcpy(out, row, kProbe * 4);
+    memcpy(out + kProbe, row + width - kProbe, kProbe * 4);
+}
+
+bool probe_equal(const float *row, uint64_t width, const float *saved) {
+    if (width < 2 * kProbe) return !memcmp(row, saved, width * 4);
+    return !memcmp(row, saved, kProbe * 4) &&
+           !memcmp(row + width - kProbe, saved + kProbe, kProbe * 4);
 }
 
 // ---------------------------------------------------------------- weights
@@ -549,7 +572,7 @@ int prepare(plamo_metal *m, struct model *model) {
             return 0;
         }
         d.synced = false;
-        d.last_kv.assign(2 * (size_t)d.width, 0.0f);
+        d.last_kv.assign(2 * probe_floats(d.width), 0.0f);
         m->max_width = std::max<uint64_t>(m->max_width, d.width);
         m->max_qkv = std::max<uint64_t>(m->max_qkv, (uint64_t)(d.qh + 2 * d.kh) * d.dim);
         m->max_attention = std::max<uint64_t>(m->max_attention, (uint64_t)d.qh * d.dim);
@@ -655,12 +678,11 @@ int sync_from_host(plamo_metal *m, struct model *model, std::vector<char> &stale
         const struct cache *c = mx->cache;
         const struct rotation *r = mx->rotation;
         uint32_t scale = float_bits(model->scales[i]);
-        const uint64_t last = c->count ? (c->count - 1) * c->width : 0;
+        const uint64_t last = c->count ? (c->count - 1) * c->width : 0, pf = probe_floats(c->width);
         bool same = d.synced && d.count == c->count && d.processed == r->processed_count &&
                     d.scale_bits == r->scale_bits &&
-                    (!c->count ||
-                     (!memcmp(c->k + last, d.last_kv.data(), c->width * 4) &&
-                      !memcmp(c->v + last, d.last_kv.data() + c->width, c->width * 4)));
+                    (!c->count || (probe_equal(c->k + last, c->width, d.last_kv.data()) &&
+                                   probe_equal(c->v + last, c->width, d.last_kv.data() + pf)));
         if (same) {
             stale[i] = r->processed_count != c->count || r->scale_bits != scale;
             continue;
@@ -689,8 +711,9 @@ void remember(plamo_metal *m, struct model *model) {
         d.processed = mx->rotation->processed_count;
         d.scale_bits = mx->rotation->scale_bits;
         if (c->count) {
-            memcpy(d.last_kv.data(), c->k + (c->count - 1) * c->width, c->width * 4);
-            memcpy(d.last_kv.data() + c->width, c->v + (c->count - 1) * c->width, c->width * 4);
+            const uint64_t last = (c->count - 1) * c->width;
+            probe_row(c->k + last, c->width, d.last_kv.data());
+            probe_row(c->v + last, c->width, d.last_kv.data() + probe_floats(c->width));
         }
         d.synced = true;
     }
@@ -729,9 +752,10 @@ int encode_decode(plamo_metal *m, struct model *model, const DecodePlan &plan, i
     int n = 0;
     float *logits = m->outbox, *state_out = m->outbox + V, *norm_out = m->outbox + V + h;
     float *stage = m->outbox + V + 2 * h;
-    HIP_TRY(m, hipMemcpyAsync(m->params_dev, m->params_host, sizeof(StepParams),
-                              hipMemcpyHostToDevice, s));
-    HIP_TRY(m, launch_embed(s, m->embedding, nullptr, m->params_dev, 1, (uint32_t)h, m->state_a));
+    // The embedding reads the host's parameter block and publishes it to the
+    // device copy the later kernels read (no separate upload node).
+    HIP_TRY(m, launch_embed(s, m->embedding, nullptr, m->params_view, 1, (uint32_t)h, m->state_a,
+                            m->params_dev));
     ++n;
     float *cur = m->state_a, *nxt = m->state_b;
     const int blocks = 2 * m->cus;
@@ -1046,6 +1070,7 @@ struct plamo_metal *plamo_metal_open(const struct plamo_metal_config *config, ch
         hipEventCreate(&m->start) != hipSuccess || hipEventCreate(&m->stop) != hipSuccess ||
         hipHostMalloc((void **)&m->params_host, sizeof(StepParams), hipHostMallocDefault) !=
             hipSuccess ||
+        !(m->params_view = (StepParams *)device_view(m->params_host)) ||
         hipHostMalloc((void **)&m->status_host, 64, hipHostMallocDefault) != hipSuccess ||
         !(m->status_dev = (uint32_t *)device_view(m->status_host)) ||
         hipMalloc((void **)&m->params_dev, sizeof(StepParams)) != hipSuccess) {

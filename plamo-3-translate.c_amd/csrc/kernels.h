@@ -46,8 +46,12 @@ struct Prologue {
 
 hipError_t launch_rope_table(hipStream_t, const float *freq, float scale, uint32_t half,
                              uint64_t first_row, uint64_t rows, float *table);
+// Row gather widened from BF16: token t reads ids[t], or params->token when
+// ids is null. With `publish`, block 0 also copies *params (a pinned host
+// block, read over the bus) to *publish for the later kernels of the step.
 hipError_t launch_embed(hipStream_t, const uint16_t *embedding, const uint32_t *ids,
-                        const StepParams *params, uint32_t tokens, uint32_t hidden, float *out);
+                        const StepParams *params, uint32_t tokens, uint32_t hidden, float *out,
+                        StepParams *publish = nullptr);
 // y[r] = W[r,:] . x (x from the prologue). swiglu_half > 0: rows r and
 // r + swiglu_half are gate/up and y[r] = silu(gate) * up for r < swiglu_half.
 hipError_t launch_gemv(hipStream_t, const uint16_t *w, uint64_t rows, uint64_t cols,

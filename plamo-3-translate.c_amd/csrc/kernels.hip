@@ -222,11 +222,22 @@ hipError_t launch_rope_table(hipStream_t stream, const float *freq, float scale,
 
 // ---------------------------------------------------------------- embedding
 // src/token.s:6-33: row gather widened from BF16.
+// A decode step's embedding also publishes the step's parameters: `publish`
+// (when non-null) is the device copy every later kernel of the step reads,
+// and `params` the host's pinned block, read here over the bus; block 0
+// copies it whole (zeroing done counts, the error word and nothing else the
+// host did not write). The step then needs no separate upload.
 __global__ __launch_bounds__(kThreads) void embed_kernel(const uint16_t *embedding,
                                                          const uint32_t *ids,
                                                          const StepParams *params,
+                                                         StepParams *publish,
                                                          uint32_t hidden, float *out) {
     uint32_t t = blockIdx.y;
+    if (publish && blockIdx.x == 0 && t == 0) {
+        const uint32_t *src = (const uint32_t *)params;
+        uint32_t *dst = (uint32_t *)publish;
+        for (uint32_t i = threadIdx.x; i < sizeof(StepParams) / 4; i += kThreads) dst[i] = src[i];
+    }
     uint32_t id = ids ? ids[t] : params->token;
     const uint16_t *row = embedding + (uint64_t)id * hidden;
     float *o = out + (uint64_t)t * hidden;
@@ -235,10 +246,12 @@ __global__ __launch_bounds__(kThreads) void embed_kernel(const uint16_t *embeddi
 }
 
 hipError_t launch_embed(hipStream_t stream, const uint16_t *embedding, const uint32_t *ids,
-                        const StepParams *params, uint32_t tokens, uint32_t hidden, float *out) {
+                        const StepParams *params, uint32_t tokens, uint32_t hidden, float *out,
+                        StepParams *publish) {
     unsigned bx = (hidden + kThreads - 1) / kThreads;
     if (bx > 16) bx = 16;
-    embed_kernel<<<dim3(bx, tokens), kThreads, 0, stream>>>(embedding, ids, params, hidden, out);
+    embed_kernel<<<dim3(bx, tokens), kThreads, 0, stream>>>(embedding, ids, params, publish, hidden,
+                                                            out);
     return hipGetLastError();
 }
 
