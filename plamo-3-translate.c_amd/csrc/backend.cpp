@@ -93,6 +93,11 @@ struct plamo_metal {
     int cus = 256;
     hipStream_t stream = nullptr;
     hipEvent_t start = nullptr, stop = nullptr;
+    // A prompt's cache rows return to the host arrays on copy_stream, layer by
+    // layer after layer_events[i] (recorded on `stream` once the layer's rows
+    // are final), overlapping the later layers.
+    hipStream_t copy_stream = nullptr;
+    hipEvent_t layer_events[kMaxLayers] = {};
     std::vector<Range> ranges;
     bool hooks = false;
 
@@ -177,6 +182,7 @@ int problem(plamo_metal *m, const char *format, ...) {
 int fail(plamo_metal *m) {
     for (Layer &l : m->layers) l.synced = false;
     if (m->stream) (void)hipStreamSynchronize(m->stream);
+    if (m->copy_stream) (void)hipStreamSynchronize(m->copy_stream);
     (void)hipGetLastError();
     return -1;
 }
@@ -1066,7 +1072,11 @@ struct plamo_metal *plamo_metal_open(const struct plamo_metal_config *config, ch
     snprintf(m->info.precision, sizeof m->info.precision, "fp32");
     snprintf(m->info.weight_storage, sizeof m->info.weight_storage, "hbm-bf16");
     m->info.recommended_working_set_bytes = prop.totalGlobalMem;
-    if (hipStreamCreateWithFlags(&m->stream, hipStreamNonBlocking) != hipSuccess ||
+    bool events = true;
+    for (hipEvent_t &e : m->layer_events)
+        events = events && hipEventCreateWithFlags(&e, hipEventDisableTiming) == hipSuccess;
+    if (!events || hipStreamCreateWithFlags(&m->stream, hipStreamNonBlocking) != hipSuccess ||
+        hipStreamCreateWithFlags(&m->copy_stream, hipStreamNonBlocking) != hipSuccess ||
         hipEventCreate(&m->start) != hipSuccess || hipEventCreate(&m->stop) != hipSuccess ||
         hipHostMalloc((void **)&m->params_host, sizeof(StepParams), hipHostMallocDefault) !=
             hipSuccess ||
@@ -1108,6 +1118,7 @@ struct plamo_metal *plamo_metal_open(const struct plamo_metal_config *config, ch
 void plamo_metal_close(struct plamo_metal *m) {
     if (!m) return;
     if (m->stream) (void)hipStreamSynchronize(m->stream);
+    if (m->copy_stream) (void)hipStreamSynchronize(m->copy_stream);
     // runtime/metal.m:938-948
     if (m->hooks && plamo_compute_context == m) {
         plamo_compute_context = nullptr;
@@ -1133,6 +1144,9 @@ void plamo_metal_close(struct plamo_metal *m) {
     if (m->start) (void)hipEventDestroy(m->start);
     if (m->stop) (void)hipEventDestroy(m->stop);
     if (m->stream) (void)hipStreamDestroy(m->stream);
+    if (m->copy_stream) (void)hipStreamDestroy(m->copy_stream);
+    for (hipEvent_t e : m->layer_events)
+        if (e) (void)hipEventDestroy(e);
     delete m;
 }
 
@@ -1302,9 +1316,11 @@ int run_prompt(plamo_metal *m, struct model *model, const uint32_t *ids, uint64_
     uint64_t split_floats = 0;
     for (uint64_t i = 0; i < L; ++i) {
         const Layer &d = m->layers[i];
+        const struct cache *c = model->layers[i]->mixer->cache;
+        const uint32_t window = c->count + T > c->capacity ? (uint32_t)c->capacity : 0;
         split_floats = std::max(split_floats,
-                                prompt_attention_scratch((uint32_t)model->layers[i]->mixer->cache->count,
-                                                         (uint32_t)T, d.qh, d.dim));
+                                prompt_attention_scratch((uint32_t)c->count, (uint32_t)T, d.qh,
+                                                         d.kh, d.dim, window));
     }
     if (split_floats && !ensure(m, m->p_attn_split, split_floats * 4)) return -1;
     for (uint64_t i = 0; i < L; ++i) {
@@ -1424,6 +1440,25 @@ int run_prompt(plamo_metal *m, struct model *model, const uint32_t *ids, uint64_
                                            d.dim));
             n += 2;
         }
+        if (!verify) {
+            // This layer's cache rows are final: they cross to the host arrays
+            // on the copy stream while the later layers compute (the appended
+            // rows, the whole window after a sliding shift, and rotations the
+            // device rebuilt).
+            const uint64_t first = overflow[i] ? 0 : c->count;
+            const uint64_t end = std::min<uint64_t>(c->count + T, c->capacity);
+            const uint64_t rot_first = (overflow[i] || stale[i]) ? 0 : first, w = d.width * 4;
+            const struct mixer *mx = model->layers[i]->mixer;
+            HIP_FAIL(m, hipEventRecord(m->layer_events[i], s));
+            HIP_FAIL(m, hipStreamWaitEvent(m->copy_stream, m->layer_events[i], 0));
+            HIP_FAIL(m, hipMemcpyAsync(c->k + first * d.width, d.k + first * d.width,
+                                       (end - first) * w, hipMemcpyDeviceToHost, m->copy_stream));
+            HIP_FAIL(m, hipMemcpyAsync(c->v + first * d.width, d.v + first * d.width,
+                                       (end - first) * w, hipMemcpyDeviceToHost, m->copy_stream));
+            HIP_FAIL(m, hipMemcpyAsync(mx->rotation->out + rot_first * d.width,
+                                       d.rot + rot_first * d.width, (end - rot_first) * w,
+                                       hipMemcpyDeviceToHost, m->copy_stream));
+        }
         // With states == NULL only the final row feeds the logits; the last
         // layer's projection and MLP run for that row alone
         // (runtime/metal_model.m:761-770).
@@ -1525,24 +1560,15 @@ int run_prompt(plamo_metal *m, struct model *model, const uint32_t *ids, uint64_
     memcpy(model->logits, m->outbox_host, V * 4);
     memcpy(model->state, m->outbox_host + V, h * 4);
     memcpy(model->normalized, m->outbox_host + V + h, h * 4);
+    if (hipStreamSynchronize(m->copy_stream) != hipSuccess) {
+        problem(m, "cannot mirror prompt KV rows");
+        return fail(m);
+    }
     for (uint64_t i = 0; i < L; ++i) {
-        Layer &d = m->layers[i];
         struct mixer *mx = model->layers[i]->mixer;
         struct cache *c = mx->cache;
         struct rotation *r = mx->rotation;
-        uint64_t first = overflow[i] ? 0 : c->count;
         uint64_t end = std::min<uint64_t>(c->count + T, c->capacity);
-        uint64_t rot_first = (overflow[i] || stale[i]) ? 0 : first;
-        uint64_t w = c->width * 4;
-        if (hipMemcpy(c->k + first * c->width, d.k + first * c->width, (end - first) * w,
-                      hipMemcpyDeviceToHost) != hipSuccess ||
-            hipMemcpy(c->v + first * c->width, d.v + first * c->width, (end - first) * w,
-                      hipMemcpyDeviceToHost) != hipSuccess ||
-            hipMemcpy(r->out + rot_first * c->width, d.rot + rot_first * c->width,
-                      (end - rot_first) * w, hipMemcpyDeviceToHost) != hipSuccess) {
-            problem(m, "cannot mirror prompt KV rows");
-            return fail(m);
-        }
         c->count = end;
         r->processed_count = end;
         r->scale_bits = float_bits(model->scales[i]);

@@ -190,7 +190,8 @@ struct PromptAttention {
 };
 hipError_t launch_prompt_attention(hipStream_t, const PromptAttention &);
 // Floats of split scratch launch_prompt_attention uses for this shape (0: none).
-uint64_t prompt_attention_scratch(uint32_t prefix, uint32_t tokens, uint32_t qh, uint32_t dim);
+uint64_t prompt_attention_scratch(uint32_t prefix, uint32_t tokens, uint32_t qh, uint32_t kh,
+                                  uint32_t dim, uint32_t window);
 
 // Rotates cache rows [0, rows) of raw K into rotated K at their row position.
 hipError_t launch_rerotate(hipStream_t, const float *k_raw, float *k_rot, const float *table,

@@ -2837,19 +2837,223 @@ static uint32_t prompt_attention_splits(uint32_t prefix, uint32_t tokens, uint32
     return (keys + rows - 1) / rows;
 }
 
-uint64_t prompt_attention_scratch(uint32_t prefix, uint32_t tokens, uint32_t qh, uint32_t dim) {
+
+// ---------------------------------------------------------------- prompt attention on matrix cores
+// The same causal attention without a sliding window, with Q K^T and P V on
+// the FP32 matrix cores (v_mfma_f32_16x16x4_f32: FP32 operands, products and
+// sums in FP32; only the summation order differs from the scalar form, as
+// it already does there). Block: KV head blockIdx.x, query tokens
+// [16 * blockIdx.y, + 16), key split blockIdx.z; wave g is query head
+// kvh * G + g, so the G heads of a group share every staged key and value
+// tile. Per tile of 32 keys a wave forms S = Q K^T for its 16 tokens (Q held
+// in registers as the A operand, K read from LDS as B), masks what the token
+// may not see, updates its running maximum and sum row by row (a token's
+// scores sit in one 16-lane row of the D layout: DPP row reductions), writes
+// P to LDS and reads it back in the A layout for O += P V.
+// D layout: lane l holds rows 4 * (l / 16) + v (v = 0..3) of column l % 16.
+constexpr int kMQ = 16, kMK = 32;
+template <int DIM>
+constexpr size_t prompt_mfma_lds(int g) {
+    return ((size_t)kMK * (DIM + 2) + (size_t)kMK * (DIM + 16) + (size_t)g * kMQ * (kMK + 2)) *
+           sizeof(float);
+}
+
+template <int DIM, int G>
+__global__ __launch_bounds__(64 * G) void prompt_attention_mfma_kernel(PromptAttention a,
+                                                                       uint32_t split_rows) {
+    constexpr int KS = DIM + 2;   // K row stride: B reads hit 32 distinct banks
+    constexpr int VS = DIM + 16;  // V row stride: the two 16-lane halves use opposite banks
+    constexpr int PS = kMK + 2;   // P row stride
+    constexpr int NT = DIM / 16;  // output column tiles of 16
+    extern __shared__ float smem[];
+    float *ks = smem;          // [kMK][KS]
+    float *vs = ks + kMK * KS; // [kMK][VS]
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    float *ps = vs + kMK * VS + wave * kMQ * PS;  // [kMQ][PS] of this wave
+    const uint32_t kvh = blockIdx.x, h = kvh * G + wave;
+    const uint32_t width = a.kh * DIM;
+    const uint32_t t0 = blockIdx.y * kMQ;
+    const uint32_t nq = a.tokens - t0 < (uint32_t)kMQ ? a.tokens - t0 : kMQ;
+    const uint32_t col = lane & 15, grp = lane >> 4;
+    // A operand of Q K^T: q[k4] = Q[token t0 + col][4 * k4 + grp] (token rows
+    // past the prompt repeat its last token; their results are dropped).
+    float q[DIM / 4];
+    {
+        const float *qrow = a.q + (uint64_t)(t0 + (col < nq ? col : nq - 1)) * a.qh * DIM +
+                            (uint64_t)h * DIM + grp;
+#pragma unroll
+        for (int k4 = 0; k4 < DIM / 4; ++k4) q[k4] = qrow[4 * k4];
+    }
+    uint32_t hi_max = a.prefix + t0 + nq, lo_min = 0;
+    if (split_rows) {
+        lo_min = blockIdx.z * split_rows;
+        hi_max = hi_max < lo_min + split_rows ? hi_max : lo_min + split_rows;
+    }
+    const float scale = 1.0f / __builtin_sqrtf((float)DIM);
+    const float ninf = -__builtin_inff();
+    f32x4 o[NT];
+#pragma unroll
+    for (int n = 0; n < NT; ++n) o[n] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    float m_run[4], l_run[4];
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+        m_run[v] = ninf;
+        l_run[v] = 0.0f;
+    }
+    for (uint32_t k0 = lo_min; k0 < hi_max; k0 += kMK) {
+        const uint32_t nk = hi_max - k0 < (uint32_t)kMK ? hi_max - k0 : kMK;
+        __syncthreads();  // the previous tile's K, V and P reads are done
+        for (uint32_t i = threadIdx.x; i < kMK * (DIM / 4); i += 64 * G) {
+            const uint32_t r = i / (DIM / 4), c = (i % (DIM / 4)) * 4;
+            const uint32_t vrow = k0 + (r < nk ? r : nk - 1);
+            const float *kp = vrow < a.prefix ? a.k_cache + (uint64_t)vrow * width
+                                              : a.k_new + (uint64_t)(vrow - a.prefix) * width;
+            const float *vp = vrow < a.prefix ? a.v_cache + (uint64_t)vrow * width
+                                              : a.v_new + (uint64_t)(vrow - a.prefix) * width;
+            f32x4 kv = *(const f32x4 *)(kp + (uint64_t)kvh * DIM + c);
+            f32x4 vv = *(const f32x4 *)(vp + (uint64_t)kvh * DIM + c);
+            if (r >= nk) kv = vv = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            float *kd = ks + r * KS + c;
+            kd[0] = kv.x; kd[1] = kv.y; kd[2] = kv.z; kd[3] = kv.w;
+            *(f32x4 *)(vs + r * VS + c) = vv;
+        }
+        __syncthreads();
+        // S for keys k0 + col and k0 + 16 + col.
+        f32x4 s0 = f32x4{0.0f, 0.0f, 0.0f, 0.0f}, s1 = s0;
+#pragma unroll
+        for (int k4 = 0; k4 < DIM / 4; ++k4) {
+            const float b0 = ks[col * KS + 4 * k4 + grp];
+            const float b1 = ks[(16 + col) * KS + 4 * k4 + grp];
+            s0 = __builtin_amdgcn_mfma_f32_16x16x4f32(q[k4], b0, s0, 0, 0, 0);
+            s1 = __builtin_amdgcn_mfma_f32_16x16x4f32(q[k4], b1, s1, 0, 0, 0);
+        }
+        float corr[4];
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const uint32_t row = 4 * grp + v;
+            const uint32_t visible = a.prefix + t0 + row + 1;  // keys of token t0 + row
+            const uint32_t r0 = k0 + col, r1 = k0 + 16 + col;
+            const bool live = row < nq;
+            const float x0 = live && col < nk && r0 < visible ? s0[v] * scale : ninf;
+            const float x1 = live && 16 + col < nk && r1 < visible ? s1[v] * scale : ninf;
+            const float m_new = fmaxf(m_run[v], row_max16(fmaxf(x0, x1)));
+            const float p0 = m_new == ninf || x0 == ninf ? 0.0f : plamo_exp(x0 - m_new);
+            const float p1 = m_new == ninf || x1 == ninf ? 0.0f : plamo_exp(x1 - m_new);
+            const float c = m_new == ninf ? 1.0f : plamo_exp(m_run[v] - m_new);
+            l_run[v] = l_run[v] * c + row_sum16(p0 + p1);
+            m_run[v] = m_new;
+            corr[v] = c;
+            ps[row * PS + col] = p0;
+            ps[row * PS + 16 + col] = p1;
+        }
+#pragma unroll
+        for (int n = 0; n < NT; ++n)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) o[n][v] = o[n][v] * corr[v];
+        __syncthreads();  // P of every wave is in LDS
+        // O += P V: A = P[token col][key 4 k4 + grp], B = V[key 4 k4 + grp][16 n + col].
+#pragma unroll
+        for (int k4 = 0; k4 < kMK / 4; ++k4) {
+            const float pa = ps[col * PS + 4 * k4 + grp];
+            const float *vrow = vs + (4 * k4 + grp) * VS + col;
+#pragma unroll
+            for (int n = 0; n < NT; ++n)
+                o[n] = __builtin_amdgcn_mfma_f32_16x16x4f32(pa, vrow[16 * n], o[n], 0, 0, 0);
+        }
+    }
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+        const uint32_t row = 4 * grp + v;
+        if (row >= nq) continue;
+        const uint32_t t = t0 + row;
+        if (split_rows) {
+            // Record [split][token][head]: unnormalized output, running max, sum.
+            float *rec = a.partial + (((uint64_t)blockIdx.z * a.tokens + t) * a.qh + h) * (DIM + 2);
+#pragma unroll
+            for (int n = 0; n < NT; ++n) rec[16 * n + col] = o[n][v];
+            if (col == 0) {
+                rec[DIM] = m_run[v];
+                rec[DIM + 1] = l_run[v];
+            }
+        } else {
+            float *out = a.out + (uint64_t)t * a.qh * DIM + (uint64_t)h * DIM;
+#pragma unroll
+            for (int n = 0; n < NT; ++n) out[16 * n + col] = o[n][v] / l_run[v];
+        }
+    }
+}
+
+static bool prompt_mfma_supported(uint32_t dim, uint32_t qh, uint32_t kh, uint32_t window) {
+    if (window || !kh || qh % kh || (dim != 64 && dim != 128)) return false;
+    const uint32_t g = qh / kh;
+    return g == 1 || g == 2 || g == 4 || g == 6 || g == 8;
+}
+
+// Key splits of the matrix-core form: only when its blocks (one per KV head
+// and 16 tokens) leave the GPU mostly idle.
+static uint32_t prompt_mfma_splits(uint32_t prefix, uint32_t tokens, uint32_t qh, uint32_t kh,
+                                   uint32_t dim, uint32_t *split_rows) {
+    const uint32_t tiles = (tokens + kMQ - 1) / kMQ, keys = prefix + tokens;
+    const uint32_t blocks = kh * tiles;
+    *split_rows = 0;
+    if (blocks >= 128 || keys <= 2 * kMK) return 1;
+    uint32_t splits = (256 + blocks - 1) / blocks;
+    splits = min(splits, min(64u, (keys + kMK - 1) / kMK));
+    while (splits > 1 && (uint64_t)splits * tokens * qh * (dim + 2) > kAttentionScratchFloats)
+        --splits;
+    if (splits <= 1) return 1;
+    uint32_t rows = (keys + splits - 1) / splits;
+    rows = (rows + kMK - 1) / kMK * kMK;
+    *split_rows = rows;
+    return (keys + rows - 1) / rows;
+}
+
+template <int DIM, int G>
+static hipError_t prompt_mfma_variant(hipStream_t stream, const PromptAttention &a, uint32_t splits,
+                                      uint32_t rows) {
+    dim3 grid(a.kh, (a.tokens + kMQ - 1) / kMQ, splits);
+    prompt_attention_mfma_kernel<DIM, G>
+        <<<grid, 64 * G, prompt_mfma_lds<DIM>(G), stream>>>(a, splits > 1 ? rows : 0);
+    return hipGetLastError();
+}
+
+template <int DIM>
+static hipError_t prompt_mfma_dim(hipStream_t stream, const PromptAttention &a, uint32_t splits,
+                                  uint32_t rows) {
+    switch (a.qh / a.kh) {
+    case 1: return prompt_mfma_variant<DIM, 1>(stream, a, splits, rows);
+    case 2: return prompt_mfma_variant<DIM, 2>(stream, a, splits, rows);
+    case 4: return prompt_mfma_variant<DIM, 4>(stream, a, splits, rows);
+    case 6: return prompt_mfma_variant<DIM, 6>(stream, a, splits, rows);
+    default: return prompt_mfma_variant<DIM, 8>(stream, a, splits, rows);
+    }
+}
+
+uint64_t prompt_attention_scratch(uint32_t prefix, uint32_t tokens, uint32_t qh, uint32_t kh,
+                                  uint32_t dim, uint32_t window) {
     uint32_t rows;
-    const uint32_t splits = prompt_attention_splits(prefix, tokens, qh, dim, &rows);
+    const uint32_t splits = prompt_mfma_supported(dim, qh, kh, window)
+                                ? prompt_mfma_splits(prefix, tokens, qh, kh, dim, &rows)
+                                : prompt_attention_splits(prefix, tokens, qh, dim, &rows);
     return splits > 1 ? (uint64_t)splits * tokens * qh * (dim + 2) : 0;
 }
 
 hipError_t launch_prompt_attention(hipStream_t stream, const PromptAttention &a) {
     if (!a.tokens) return hipSuccess;
-    size_t lds = (kQT * a.dim + kKT * (a.dim + 1) + kKT * a.dim + kQT * kKT + 3 * kQT) * sizeof(float);
-    uint32_t rows = 0;
-    uint32_t splits = a.partial ? prompt_attention_splits(a.prefix, a.tokens, a.qh, a.dim, &rows) : 1;
-    dim3 grid(a.qh, (a.tokens + kQT - 1) / kQT, splits);
-    prompt_attention_kernel<<<grid, kThreads, lds, stream>>>(a, splits > 1 ? rows : 0);
+    uint32_t rows = 0, splits = 1;
+    hipError_t e;
+    if (prompt_mfma_supported(a.dim, a.qh, a.kh, a.window)) {
+        if (a.partial) splits = prompt_mfma_splits(a.prefix, a.tokens, a.qh, a.kh, a.dim, &rows);
+        e = a.dim == 64 ? prompt_mfma_dim<64>(stream, a, splits, rows)
+                        : prompt_mfma_dim<128>(stream, a, splits, rows);
+    } else {
+        size_t lds = (kQT * a.dim + kKT * (a.dim + 1) + kKT * a.dim + kQT * kKT + 3 * kQT) * sizeof(float);
+        if (a.partial) splits = prompt_attention_splits(a.prefix, a.tokens, a.qh, a.dim, &rows);
+        dim3 grid(a.qh, (a.tokens + kQT - 1) / kQT, splits);
+        prompt_attention_kernel<<<grid, kThreads, lds, stream>>>(a, splits > 1 ? rows : 0);
+        e = hipGetLastError();
+    }
+    if (e != hipSuccess) return e;
     if (splits > 1)
         attention_merge_kernel<<<a.tokens * a.qh, 128, 0, stream>>>(
             a.partial, splits, (uint64_t)a.tokens * a.qh * (a.dim + 2), a.dim, a.out);
