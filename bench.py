@@ -67,9 +67,10 @@ def restore(inst: plamo_hip.Instance, snap, rows: int):
         inst.rotation(i).scale_bits = scale
 
 
-def prefill_flop(cfg: dict, prefix: int, tokens: int) -> float:
-    """Linear-layer FLOP of a prompt (2 per weight per token; the last layer's
-    O/MLP and the head run for the final row only) plus attention FLOP."""
+def prefill_flop_parts(cfg: dict, prefix: int, tokens: int) -> tuple[float, float]:
+    """(linear, attention) FLOP of a prompt: 2 per weight per token for the
+    projections (the last layer's O/MLP and the head run for the final row
+    only), 4 * dim per visible key per query head for Q K^T and P V."""
     h, d, qh, kh, inter, L = (cfg[k] for k in ("hidden", "dim", "qh", "kh", "intermediate",
                                                  "layers"))
     qkv = (qh + 2 * kh) * d * h
@@ -77,7 +78,31 @@ def prefill_flop(cfg: dict, prefix: int, tokens: int) -> float:
     linear = 2.0 * (qkv * tokens * L + rest * (tokens * (L - 1) + 1) + cfg["vocab"] * h)
     keys = sum(prefix + t + 1 for t in range(tokens))
     attention = 4.0 * qh * d * keys * L
-    return linear + attention
+    return linear, attention
+
+
+def prefill_flop(cfg: dict, prefix: int, tokens: int) -> float:
+    return sum(prefill_flop_parts(cfg, prefix, tokens))
+
+
+def prefill_roofline(cfg: dict, prefix: int, tokens: int, ttft_ms: float) -> dict:
+    """The prefill against the ceilings of the instructions it runs: the
+    projections on the BF16 matrix cores with three products per FP32 input
+    (2.5 PFLOP/s / 3), attention on the FP32 matrix cores (157.3 TFLOP/s),
+    and the weights crossing HBM once (8 TB/s) as a floor."""
+    linear, attention = prefill_flop_parts(cfg, prefix, tokens)
+    mfma_ms = (linear / (SPLIT_BF16_CEILING_TFLOPS * 1e12) +
+               attention / (FP32_MFMA_PEAK_TFLOPS * 1e12)) * 1e3
+    hbm_ms = plamo_hip.weight_bytes_per_step(cfg) / (HBM_PEAK_GBPS * 1e9) * 1e3
+    bound_ms = max(mfma_ms, hbm_ms)
+    flop = linear + attention
+    return {"tokens_after_prefix": tokens, "flop": flop, "linear_flop": linear,
+            "attention_flop": attention, "achieved_TFLOPs": round(flop / ttft_ms / 1e9, 2),
+            "mfma_bound_ms": round(mfma_ms, 3), "hbm_bound_ms": round(hbm_ms, 3),
+            "bound": "mfma" if mfma_ms >= hbm_ms else "hbm",
+            "frac": round(bound_ms / ttft_ms, 4),
+            "note": "frac = max(linear / 833.3 TFLOP/s (split BF16) + attention / 157.3 TFLOP/s "
+                    "(FP32 MFMA), weights / 8 TB/s) / TTFT"}
 
 
 def host_threads() -> tuple[int, int]:
@@ -398,6 +423,9 @@ def main() -> int:
     ap.add_argument("--verify", action="store_true",
                     help="time the C5 target's batched verify alone, per candidate count")
     ap.add_argument("--verify-tokens", default="1,2,3,4,5,6,8,16")
+    ap.add_argument("--prefill-only", action="store_true",
+                    help="measure TTFT for --ttft-sizes only (one JSON line, no decode)")
+    ap.add_argument("--ttft-runs", type=int, default=12)
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path "
@@ -436,14 +464,30 @@ def main() -> int:
     ttft = {}
     for n in [int(x) for x in args.ttft_sizes.split(",") if x]:
         times = []
-        for _ in range(12):
+        for _ in range(args.ttft_runs):
             start = time.perf_counter()
             restore(inst, snap, PREFIX)
             if be.prefill(inst, prompt[PREFIX:n]) != 1:
                 raise RuntimeError(be.info().note.decode())
             times.append(time.perf_counter() - start)
-        ttft[n] = float(np.median(times[4:])) * 1e3
+        ttft[n] = float(np.median(times[min(4, len(times) - 1):])) * 1e3
         log(f"TTFT {n} tokens: {ttft[n]:.2f} ms (runs {[round(t * 1e3, 2) for t in times]})")
+    if args.prefill_only:
+        info = be.info()
+        assert info.errors == 0 and info.cpu_fallbacks == 0, info.note.decode()
+        be.close()
+        inst.close()
+        syn.close()
+        print(json.dumps({
+            "metric": "prefill TTFT (12-token prefix restored)", "unit": "ms",
+            "higher_is_better": False, "n_gpus": 1, "dtype": "fp32",
+            "data": "synthetic (seeded BF16 weights ~N(0,0.02), uniform random prompt ids)",
+            "config": {"workload": f"{args.config}: prompt body after a {PREFIX}-token prefix"},
+            "ttft_ms": {str(k): round(v, 3) for k, v in ttft.items()},
+            "prefill_roofline": {str(n): prefill_roofline(plamo_hip.CONFIGS[args.config], PREFIX,
+                                                          n - PREFIX, ttft[n]) for n in ttft}}),
+            flush=True)
+        return 0
 
     # Decode: prompt of args.prompt tokens, then greedy steps.
     restore(inst, snap, PREFIX)
@@ -484,7 +528,6 @@ def main() -> int:
 
     if args.copy_calibration:
         copy_calibration(args.copy_calibration << 20)
-    ttft_flop = prefill_flop(plamo_hip.CONFIGS[args.config], PREFIX, 128 - PREFIX)
     traffic = measured_traffic()
     result = {
         "metric": "decode tok/s + % HBM roofline (8B-class, bs=1); prefill TTFT @128 tok",
@@ -510,15 +553,8 @@ def main() -> int:
                               "frac": round(step_bytes / ms_step / 1e6 / HBM_PEAK_GBPS, 4),
                               "gpu_ms_per_step": round(gpu_ms_step, 4)},
         "ttft_ms": {str(k): round(v, 3) for k, v in ttft.items()},
-        "prefill_roofline_128": ({"flop": ttft_flop,
-                                  "achieved_TFLOPs": round(ttft_flop / ttft[128] / 1e9, 2),
-                                  "peak_TFLOPs": FP32_MFMA_PEAK_TFLOPS,
-                                  "frac": round(ttft_flop / ttft[128] / 1e9 /
-                                                FP32_MFMA_PEAK_TFLOPS, 4),
-                                  "split_bf16_ceiling_TFLOPs": SPLIT_BF16_CEILING_TFLOPS,
-                                  "frac_of_split_bf16": round(ttft_flop / ttft[128] / 1e9 /
-                                                              SPLIT_BF16_CEILING_TFLOPS, 4)}
-                                 if 128 in ttft else None),
+        "prefill_roofline": {str(n): prefill_roofline(plamo_hip.CONFIGS[args.config], PREFIX,
+                                                      n - PREFIX, ttft[n]) for n in ttft},
         "roofline": {"bound": "hbm", "kernel": "gemv_regp_kernel<8,2,SWIGLU> (gate/up + SwiGLU)",
                      "achieved": dom["GBps"], "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(dom["GBps"] / HBM_PEAK_GBPS, 4), "traffic": traffic},
