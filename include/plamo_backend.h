@@ -19,17 +19,22 @@
 #ifndef PLAMO_BACKEND_H
 #define PLAMO_BACKEND_H
 #include "plamo_model.h"
+#include "plamo_parallel.h"
 
 #ifdef __cplusplus
 extern "C" {
 #endif
 
-/* runtime/weight_cache.h:7-11 */
+/* runtime/weight_cache.h:7-11. A translation unit that includes the engine's
+ * runtime/weight_cache.h first (as runtime/metal.h:3-4 does) keeps its
+ * definition. */
+#ifndef PLAMO_WEIGHT_CACHE_H
 struct plamo_weight_cache_info {
     uint64_t budget_bytes, max_budget_bytes, cached_bytes, staging_bytes;
     uint64_t hits, hit_bytes, misses, resizes;
     uint64_t storage_bytes;
 };
+#endif
 
 /* runtime/metal.h:6-13 */
 enum plamo_metal_memory { PLAMO_METAL_AUTO, PLAMO_METAL_RESIDENT, PLAMO_METAL_STREAM };

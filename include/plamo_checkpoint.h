@@ -124,18 +124,15 @@ const struct plamo_weight_spec *plamo_checkpoint_schema(const struct plamo_check
 struct plamo_synthetic_instance *plamo_checkpoint_instantiate(const struct plamo_checkpoint *,
                                                               int pinned, char *error, size_t cap);
 
-/* ---- the engine's model globals (runtime/model.h:88-101, src/model_open.s) ----
+/* ---- the engine's model globals (declared in plamo_model.h) ----
  * plamo_model_open() opens the directory set by plamo_model_set_directory(), or
- * else $PLAMO_MODEL_DIR, once per process, and fills these globals for
- * runtime/engine.c. 1 = ready (repeat calls succeed at once), 0 = failure. */
-enum { PLAMO_MAX_WEIGHT_FILES = 64, PLAMO_MAX_SCHEMA = 3 + 10 * 128 + 1 };
-extern struct model plamo_model;
-extern struct plamo_mapping plamo_weight_mappings[PLAMO_MAX_WEIGHT_FILES];
-extern int64_t plamo_weight_fds[PLAMO_MAX_WEIGHT_FILES];
-extern uint64_t plamo_weight_mapping_count, plamo_weight_file_count;
-extern struct plamo_weight_spec plamo_weight_schema[PLAMO_MAX_SCHEMA];
+ * else $PLAMO_MODEL_DIR, and fills plamo_model, the weight tables, the schema
+ * (at most PLAMO_MAX_SCHEMA entries with its terminator) and the patch table.
+ * plamo_model_set_directory() also sets the profile strings at once (the
+ * engine opens the tokenizer before the model, runtime/engine.c:113); 0 when
+ * the path is too long or a model is already open. */
+enum { PLAMO_MAX_SCHEMA = 3 + 10 * 128 + 1 };
 int plamo_model_set_directory(const char *directory);
-int plamo_model_open(void);
 
 #ifdef __cplusplus
 }

@@ -17,6 +17,7 @@
 #ifndef PLAMO_COMPUTE_H
 #define PLAMO_COMPUTE_H
 #include "plamo_model.h"
+#include "plamo_parallel.h"
 
 #ifdef __cplusplus
 extern "C" {
@@ -31,11 +32,10 @@ extern int (*plamo_mlp_kernel)(const struct mlp *, float *, uint64_t, void *);
 extern int (*plamo_forward_kernel)(struct model *, uint64_t, void *);
 extern int (*plamo_prefill_kernel)(struct model *, const uint32_t *, uint64_t, float *, void *);
 
-/* runtime/model.h:63-66 (storage src/prefetch.s:31-36): optional weight provider.
- * The GPU backend installs the identity provider with chunk bytes 0. */
-extern const void *(*plamo_weight_provider)(const void *, uint64_t, void *);
-extern void *plamo_weight_context;
-extern uint64_t plamo_weight_chunk_bytes;
+/* The optional weight provider (plamo_weight_provider, plamo_weight_context,
+ * plamo_weight_chunk_bytes) is declared with the model globals in
+ * plamo_model.h. The GPU backend installs the identity provider with chunk
+ * bytes 0. */
 
 /* The platform CPU path behind the trampolines. On the reference platform this
  * is the AArch64 assembly (src/forward.s:33-81, src/prefill.s:31-178); this

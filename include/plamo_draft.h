@@ -18,7 +18,9 @@
 extern "C" {
 #endif
 
-enum { PLAMO_DRAFT_MAX = 16 }; /* runtime/draft.h:5 */
+/* runtime/draft.h:5. The magic tags the reference's draft-pipe frames; the
+ * in-process proposer has no pipe and never sends one. */
+enum { PLAMO_DRAFT_MAX = 16, PLAMO_DRAFT_MAGIC = 0x504c4431 };
 
 struct plamo_draft;
 

@@ -7,7 +7,7 @@
  *   - struct qkv/cache/rotation/gqa/mixer/mlp/layer/model:
  *       runtime/model.h:7-60 (sizes asserted at runtime/model.h:76-86)
  *   - struct plamo_mapping / plamo_weight_spec: runtime/model.h:61-70
- *   - struct plamo_matmul: runtime/parallel.h:5-10
+ *   - struct plamo_matmul: runtime/parallel.h:5-10, declared in plamo_parallel.h
  *
  * Conventions (all from the reference):
  *   - weights are BF16 bit patterns (uint16_t), row-major [rows, columns];
@@ -92,13 +92,6 @@ struct plamo_weight_spec {
     const uint64_t *shape;
     void **slot;
 };
-/* runtime/parallel.h:5-10: strides are in FP32 elements. */
-struct plamo_matmul {
-    const uint16_t *weights;
-    const float *input;
-    float *output;
-    uint64_t rows, columns, tokens, input_stride, output_stride;
-};
 
 #ifdef __cplusplus
 #define PLAMO_STATIC_ASSERT static_assert
@@ -116,7 +109,45 @@ PLAMO_STATIC_ASSERT(sizeof(struct layer) == 64, "descriptor ABI: layer");
 PLAMO_STATIC_ASSERT(offsetof(struct layer, mixer) == 40, "descriptor ABI: layer");
 PLAMO_STATIC_ASSERT(offsetof(struct cache, count) == 24, "descriptor ABI: cache");
 PLAMO_STATIC_ASSERT(offsetof(struct rotation, processed_count) == 56, "descriptor ABI: rotation");
-PLAMO_STATIC_ASSERT(sizeof(struct plamo_matmul) == 64, "descriptor ABI: matmul");
+
+/* The engine's model globals (runtime/model.h:88-101). The reference
+ * generates them into assembly from a model profile at build time
+ * (tools/generate_model.py:20-41, src/model_layout.s, src/prefetch.s); this
+ * library fills them at run time from a checkpoint directory
+ * (plamo_model_set_directory() in plamo_checkpoint.h, or $PLAMO_MODEL_DIR read
+ * when the library loads), so the four strings are writable arrays here:
+ *   plamo_vocab_path        <directory>/tokenizer.jsonl;
+ *   plamo_model_name        "plamo-3-translate-<size>" when config.json has the
+ *                           shape of a published profile (tools/profiles/<size>),
+ *                           else "plamo-3-translate-custom";
+ *   plamo_model_repository, plamo_model_revision  the profile's manifest values,
+ *                           else empty. */
+enum { PLAMO_MAX_WEIGHT_FILES = 64 };
+extern struct model plamo_model;
+extern struct plamo_mapping plamo_weight_mappings[PLAMO_MAX_WEIGHT_FILES];
+extern int64_t plamo_weight_fds[PLAMO_MAX_WEIGHT_FILES];
+extern uint64_t plamo_weight_mapping_count, plamo_weight_file_count;
+extern char plamo_vocab_path[], plamo_model_name[], plamo_model_repository[],
+    plamo_model_revision[];
+extern struct plamo_weight_spec plamo_weight_schema[];
+/* plamo_model_patches: {descriptor field address, schema slot address} pairs,
+ * terminated by a zero pair, filled by plamo_model_open(). plamo_io_policy and
+ * plamo_io_stats[4] ({bytes staged, read calls, ...}, src/prefetch.s:28-66)
+ * are kept for the engine: the GPU path reads no weight file during a token,
+ * so the statistics stay zero. */
+extern uint64_t plamo_model_patches[], plamo_io_policy, plamo_io_stats[4];
+/* runtime/model.h:97-100 (storage src/prefetch.s:31-36). */
+extern const void *(*plamo_weight_provider)(const void *, uint64_t, void *);
+extern void *plamo_weight_context;
+extern uint64_t plamo_weight_chunk_bytes;
+/* src/model_open.s:6-60: opens the model directory once per process.
+ * 1 = ready (repeat calls succeed at once), 0 = failure (message on stderr). */
+int plamo_model_open(void);
+/* src/model_init.s:1-25: for a patch table as above, 1 after storing every
+ * slot's pointer into its descriptor field, or 0 with nothing stored when a
+ * slot holds NULL. The engine calls it after moving the weights
+ * (runtime/engine.c:69-74). */
+int plamo_model_patch(void *patches);
 
 /* Token-loop entry points of the compute dispatch layer (runtime/model.h:103-105,
  * src/forward.s:9-31, src/prefill.s:7-30, src/token.s:37-63). The trampolines

@@ -13,6 +13,7 @@
 #ifndef PLAMO_ORACLE_H
 #define PLAMO_ORACLE_H
 #include "../include/plamo_model.h"
+#include "../include/plamo_parallel.h"
 
 #ifdef __cplusplus
 extern "C" {

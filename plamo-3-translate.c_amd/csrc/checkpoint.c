@@ -817,28 +817,134 @@ struct plamo_mapping plamo_weight_mappings[PLAMO_MAX_WEIGHT_FILES];
 int64_t plamo_weight_fds[PLAMO_MAX_WEIGHT_FILES];
 uint64_t plamo_weight_mapping_count, plamo_weight_file_count;
 struct plamo_weight_spec plamo_weight_schema[PLAMO_MAX_SCHEMA];
+char plamo_vocab_path[4096 + 32], plamo_model_name[64] = "plamo-3-translate-custom",
+                                  plamo_model_repository[80], plamo_model_revision[64];
+/* Pairs plus the zero terminator: one descriptor field per schema entry (the
+ * tied head reuses the embedding's slot in place of its own entry). */
+uint64_t plamo_model_patches[2 * PLAMO_MAX_SCHEMA];
+uint64_t plamo_io_policy, plamo_io_stats[4];
 
 static char model_directory[4096];
 static struct plamo_checkpoint *opened;
 static struct plamo_synthetic_instance *opened_instance;
 
+/* The published profiles (tools/profiles/{0.8b,2b,8b,31b}/config.json shapes
+ * and manifest.json repository revisions): the engine keys behaviour on the
+ * name (runtime/engine.c:146-149, 322-324). */
+static const struct {
+    uint64_t hidden, layers, qh, kh, intermediate;
+    int tied;
+    const char *size, *revision;
+} profiles[] = {
+    {1536, 16, 16, 1, 6144, 0, "0.8b", "573eb1be9fd8c44402650810c680104e5aec81e8"},
+    {2560, 24, 24, 4, 10240, 0, "2b", "78355e2f59605d1c2c7c46e915333ffded24c8ff"},
+    {4096, 32, 32, 4, 16384, 0, "8b", "19ecab3fb31424ee937b7503730318b50e55771c"},
+    {5120, 64, 64, 8, 25600, 1, "31b", "d6743d65c2cc61a07ff0fb2c3ff3cf7fd8ca36eb"},
+};
+
+static void set_profile_strings(const char *directory) {
+    snprintf(plamo_vocab_path, sizeof plamo_vocab_path, "%s/tokenizer.jsonl", directory);
+    snprintf(plamo_model_name, sizeof plamo_model_name, "plamo-3-translate-custom");
+    plamo_model_repository[0] = plamo_model_revision[0] = 0;
+    char path[4096 + 16], error[256];
+    snprintf(path, sizeof path, "%s/config.json", directory);
+    size_t size = 0;
+    char *text = read_text(path, &size);
+    struct plamo_checkpoint_config c;
+    if (!text)
+        return;
+    const int ok = read_config(text, size, &c, error, sizeof error);
+    free(text);
+    for (size_t i = 0; ok && i < sizeof profiles / sizeof *profiles; ++i)
+        if (profiles[i].hidden == c.hidden && profiles[i].layers == c.layers &&
+            profiles[i].qh == c.qh && profiles[i].kh == c.kh &&
+            profiles[i].intermediate == c.intermediate && profiles[i].tied == c.tied) {
+            snprintf(plamo_model_name, sizeof plamo_model_name, "plamo-3-translate-%s",
+                     profiles[i].size);
+            snprintf(plamo_model_repository, sizeof plamo_model_repository, "pfnet/%s",
+                     plamo_model_name);
+            snprintf(plamo_model_revision, sizeof plamo_model_revision, "%s", profiles[i].revision);
+        }
+}
+
 int plamo_model_set_directory(const char *directory) {
     if (!directory || strlen(directory) >= sizeof model_directory || opened)
         return 0;
     strcpy(model_directory, directory);
+    set_profile_strings(directory);
     return 1;
+}
+
+/* The generated profile is part of the reference binary, so its strings exist
+ * before main(); here $PLAMO_MODEL_DIR plays that part when the library loads. */
+__attribute__((constructor)) static void model_directory_from_environment(void) {
+    const char *dir = getenv("PLAMO_MODEL_DIR");
+    if (dir && *dir)
+        (void)plamo_model_set_directory(dir);
+}
+
+/* src/model_init.s:1-25: check every slot, then store. */
+int plamo_model_patch(void *patches) {
+    const uint64_t *p = patches;
+    for (const uint64_t *q = p; q[0]; q += 2)
+        if (!*(void *const *)(uintptr_t)q[1])
+            return 0;
+    for (; p[0]; p += 2)
+        *(void **)(uintptr_t)p[0] = *(void *const *)(uintptr_t)p[1];
+    return 1;
+}
+
+/* The descriptor fields each schema entry feeds, in build_schema's order. */
+static void build_patches(const struct plamo_checkpoint *ck, struct model *m) {
+    const struct plamo_checkpoint_config *c = &ck->config;
+    size_t n = 0;
+#define PATCH(field, entry)                                                                        \
+    do {                                                                                           \
+        plamo_model_patches[2 * n] = (uint64_t)(uintptr_t) & (field);                              \
+        plamo_model_patches[2 * n + 1] = (uint64_t)(uintptr_t)ck->schema[entry].slot;              \
+        ++n;                                                                                       \
+    } while (0)
+    PATCH(m->embedding, 0);
+    PATCH(m->norm, 1);
+    PATCH(m->head, c->tied ? 0 : 2);
+    const size_t base = c->tied ? 2 : 3;
+    for (uint64_t i = 0; i < c->layers; ++i) {
+        struct layer *l = m->layers[i];
+        const size_t e = base + 10 * i;
+        PATCH(l->mixer->qkv->weight, e + 0);
+        PATCH(l->mixer->weight, e + 1);
+        PATCH(l->mixer->qkv->qn, e + 2);
+        PATCH(l->mixer->qkv->kn, e + 3);
+        PATCH(l->mlp->gu, e + 4);
+        PATCH(l->mlp->down, e + 5);
+        PATCH(l->pre, e + 6);
+        PATCH(l->post, e + 7);
+        PATCH(l->mlp->pre, e + 8);
+        PATCH(l->mlp->post, e + 9);
+    }
+#undef PATCH
+    plamo_model_patches[2 * n] = plamo_model_patches[2 * n + 1] = 0;
 }
 
 int plamo_model_open(void) {
     if (opened)
         return 1;
     const char *dir = model_directory[0] ? model_directory : getenv("PLAMO_MODEL_DIR");
-    if (!dir)
+    if (!dir) {
+        fprintf(stderr, "plamo_model_open: no model directory (plamo_model_set_directory or "
+                        "PLAMO_MODEL_DIR)\n");
         return 0;
+    }
     char error[512];
     struct plamo_checkpoint *ck = plamo_checkpoint_open(dir, 0, error, sizeof error);
     if (!ck) {
         fprintf(stderr, "plamo_model_open: %s\n", error);
+        return 0;
+    }
+    if (ck->config.layers > (PLAMO_MAX_SCHEMA - 4) / 10) {
+        fprintf(stderr, "plamo_model_open: %llu layers exceed the engine tables\n",
+                (unsigned long long)ck->config.layers);
+        plamo_checkpoint_close(ck);
         return 0;
     }
     /* Page-locked host arrays when the runtime grants them (the backend then
@@ -851,6 +957,8 @@ int plamo_model_open(void) {
         plamo_checkpoint_close(ck);
         return 0;
     }
+    if (!model_directory[0])
+        set_profile_strings(dir);
     plamo_model = *plamo_synthetic_model(in);
     for (size_t i = 0; i < ck->count; ++i) {
         plamo_weight_mappings[i] = ck->maps[i];
@@ -858,9 +966,10 @@ int plamo_model_open(void) {
     }
     plamo_weight_mapping_count = plamo_weight_file_count = ck->count;
     size_t n = 0;
-    for (const struct plamo_weight_spec *s = ck->schema; s->name && n + 1 < PLAMO_MAX_SCHEMA; ++s)
+    for (const struct plamo_weight_spec *s = ck->schema; s->name; ++s)
         plamo_weight_schema[n++] = *s;
     plamo_weight_schema[n] = (struct plamo_weight_spec){0};
+    build_patches(ck, &plamo_model);
     opened = ck;
     opened_instance = in;
     return 1;

@@ -23,7 +23,7 @@ def run(*args, env=None):
     if not CLI.exists():
         pytest.fail(f"{CLI} is not built (make -C plamo-3-translate.c_amd/csrc)")
     return subprocess.run([str(CLI), *args], capture_output=True, text=True, timeout=120,
-                          env=env)
+                          env=env, stdin=subprocess.DEVNULL)
 
 
 def test_usage_and_argument_errors():
@@ -64,3 +64,25 @@ def test_checkpoint_on_a_host_without_gpu(tmp_path):
     assert r.returncode == 1
     assert "MI355X" in r.stderr
     assert r.stdout == ""
+
+
+def test_worker_startup_without_gpu(tmp_path):
+    """--worker reports a failed start as the reference worker does
+    (runtime/worker.c:413-420): one error event, status 1. Ids on the command
+    line are a usage error in worker mode."""
+    r = run("--worker", "5")
+    assert r.returncode == 2 and r.stderr.startswith("usage: plamo-hip")
+    syn = plamo_hip.Synthetic(256, 2, 2, 1, 128, 512, 300, window=4, global_capacity=32,
+                              pattern=2, seed=3)
+    try:
+        directory = checkpoint_writer.write(tmp_path / "ck", syn, shards=1)
+    finally:
+        syn.close()
+    r = run("--worker", "--model", str(directory))
+    if r.returncode == 0:
+        pytest.skip("a GPU is visible: the worker is covered by test_gpu_cli.py")
+    assert r.returncode == 1
+    import json
+    event = json.loads(r.stdout)
+    assert event["event"] == "error" and event["code"] == "startup_failed"
+    assert "MI355X" in event["message"]
