@@ -622,7 +622,11 @@ __global__ __launch_bounds__(kThreads) void gemv_reg_kernel(const uint16_t *__re
 // rows per step; with SWIGLU the step is the pair (gate row p, up row
 // p + half) and the output silu(gate) * up (tests/activation_reference.s:99-126).
 // The first rows' weights are requested before the prologue's reductions.
-template <int KC, int U, bool SWIGLU, int WPR = 1>
+// With PF each wave requests its next step's weights before computing the
+// current one (two register sets), so a wave never waits on a load it could
+// have issued a step earlier; it pays where the second set does not lower
+// the waves a SIMD holds.
+template <int KC, int U, bool SWIGLU, int WPR = 1, bool PF = false>
 __global__ __launch_bounds__(kThreads) void gemv_regp_kernel(const uint16_t *__restrict__ w,
                                                              uint64_t rows, uint64_t cols,
                                                              Prologue pro, float *__restrict__ y,
@@ -649,9 +653,9 @@ __global__ __launch_bounds__(kThreads) void gemv_regp_kernel(const uint16_t *__r
     prologue_begin(pro, n, pp);
     prologue_load(pro, pp);
     __builtin_amdgcn_sched_barrier(0);
-    u32x4 wv[U][KC];
+    u32x4 wa[U][KC], wb[PF ? U : 1][PF ? KC : 1];
     const uint32_t last = (uint32_t)rows - 1, uhalf = (uint32_t)half;
-    auto load = [&](uint32_t unit) {
+    auto load = [&](uint32_t unit, auto &wv) {
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             uint32_t r = SWIGLU ? unit + u * uhalf : unit * U + u;
@@ -661,7 +665,7 @@ __global__ __launch_bounds__(kThreads) void gemv_regp_kernel(const uint16_t *__r
             for (int c = 0; c < KC; ++c) wv[u][c] = __builtin_nontemporal_load(p + c * 64);
         }
     };
-    if (u0 < units) load(u0);
+    if (u0 < units) load(u0, wa);
     __builtin_amdgcn_sched_barrier(0);
     prologue_finish(pro, n, pp, xs, red, bid);
     publish_status(pro, bid);
@@ -673,11 +677,8 @@ __global__ __launch_bounds__(kThreads) void gemv_regp_kernel(const uint16_t *__r
         x[c][0] = a.x; x[c][1] = a.y; x[c][2] = a.z; x[c][3] = a.w;
         x[c][4] = b.x; x[c][5] = b.y; x[c][6] = b.z; x[c][7] = b.w;
     }
-    // With WPR > 1 every wave of the block runs every trip (barriers inside).
-    for (uint32_t ub = ubase; WPR == 1 ? ub + grp < units : ub < units; ub += step) {
-        const uint32_t unit = ub + grp;
+    auto compute = [&](const auto &wv, uint32_t unit) {
         const bool valid = unit < units;
-        if (ub != ubase && valid) load(unit);
         float acc[U];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
@@ -716,6 +717,26 @@ __global__ __launch_bounds__(kThreads) void gemv_regp_kernel(const uint16_t *__r
                 for (int u = 0; u < U; ++u)
                     if (unit * U + u < rows) y[unit * U + u] = acc[u];
             }
+        }
+    };
+    // With WPR > 1 every wave of the block runs every trip (barriers inside),
+    // so the trip condition depends on the block only.
+    auto more = [&](uint32_t ub) { return WPR == 1 ? ub + grp < units : ub < units; };
+    if constexpr (!PF) {
+        for (uint32_t ub = ubase; more(ub); ub += step) {
+            const uint32_t unit = ub + grp;
+            if (ub != ubase && unit < units) load(unit, wa);
+            compute(wa, unit);
+        }
+    } else {
+        // Two trips per iteration, the register sets alternating.
+        for (uint32_t ub = ubase; more(ub); ub += 2 * step) {
+            const uint32_t ua = ub + grp, ubn = ua + step;
+            if (ubn < units) load(ubn, wb);
+            compute(wa, ua);
+            if (!more(ub + step)) break;
+            if (ubn + step < units) load(ubn + step, wa);
+            compute(wb, ubn);
         }
     }
 }
@@ -783,7 +804,7 @@ static hipError_t gemv_variant(hipStream_t stream, const uint16_t *w, uint64_t r
 // Register-x prologue GEMV for widths of whole 512-column chunks (KC chunks
 // per wave, WPR waves per step). Grid: one step (U rows or a gate/up pair) per
 // wave group at most, capped at the blocks the GPU holds at once.
-template <int KC, int WPR = 1>
+template <int KC, int WPR = 1, bool PF = false>
 static hipError_t regp_variant(hipStream_t stream, const uint16_t *w, uint64_t rows,
                                uint64_t cols, const Prologue &pro, float *y, uint64_t half,
                                int blocks_hint) {
@@ -799,9 +820,9 @@ static hipError_t regp_variant(hipStream_t stream, const uint16_t *w, uint64_t r
     if (blocks > cap) blocks = cap;
     const size_t lds = cols * sizeof(float);
     if (half)
-        gemv_regp_kernel<KC, 2, true, WPR><<<(unsigned)blocks, kThreads, lds, stream>>>(w, rows, cols, pro, y, half);
+        gemv_regp_kernel<KC, 2, true, WPR, PF><<<(unsigned)blocks, kThreads, lds, stream>>>(w, rows, cols, pro, y, half);
     else
-        gemv_regp_kernel<KC, 2, false, WPR><<<(unsigned)blocks, kThreads, lds, stream>>>(w, rows, cols, pro, y, 0);
+        gemv_regp_kernel<KC, 2, false, WPR, PF><<<(unsigned)blocks, kThreads, lds, stream>>>(w, rows, cols, pro, y, 0);
     return hipGetLastError();
 }
 
@@ -813,7 +834,7 @@ static bool regp_launch(hipStream_t stream, const uint16_t *w, uint64_t rows, ui
     case 4: *status = regp_variant<4>(stream, w, rows, cols, pro, y, half, blocks_hint); return true;
     case 5: *status = regp_variant<5>(stream, w, rows, cols, pro, y, half, blocks_hint); return true;
     case 8: *status = regp_variant<8>(stream, w, rows, cols, pro, y, half, blocks_hint); return true;
-    case 12: *status = regp_variant<6, 2>(stream, w, rows, cols, pro, y, half, blocks_hint); return true;
+    case 12: *status = regp_variant<6, 2, true>(stream, w, rows, cols, pro, y, half, blocks_hint); return true;
     default: return false;
     }
 }
