@@ -67,6 +67,32 @@ def test_exp_against_libm(oracle):
     assert oracle.oracle_exp(float("nan")) == 0.0
 
 
+def test_exp_polynomial_terms(oracle):
+    """The reference's exponential (src/activation.s, tests/activation_reference.s:
+    8-50) reduces x = n ln2 + r, |r| <= ln2/2, and evaluates a degree-7
+    polynomial. Its worst relative error over [-86, 87] is 3.0e-7 (FP32
+    rounding); a dropped r^6 term would add up to 1.7e-6, so 4e-7 pins it. The
+    r^7 term is worth at most 8.4e-8 relative at |r| = ln2/2, within the
+    rounding of a single value, but not on average: at inputs with r in
+    [0.30, 0.345] the signed error a/exp(x) - 1 averages zero, and without the
+    r^7 term it would average about -5e-8 (that term's mean over the range)."""
+    worst = 0.0
+    for i in range(-860000, 870001, 97):
+        x = float(np.float32(i / 10000.0))
+        worst = max(worst, abs(oracle.oracle_exp(x) / math.exp(x) - 1))
+    assert worst <= 4e-7
+    ln2 = math.log(2.0)
+    signed = []
+    for k in range(-120, 121):
+        for j in range(40):
+            x = float(np.float32(k * ln2 + 0.30 + 0.045 * j / 40))
+            r = x - round(x / ln2) * ln2
+            if 0.30 <= r <= 0.345 and -86 < x < 87:
+                signed.append(oracle.oracle_exp(x) / math.exp(x) - 1)
+    assert len(signed) > 5000
+    assert abs(float(np.mean(signed))) < 2e-8
+
+
 def test_softmax_and_swiglu(oracle):
     # tests/activation.c:14-26
     x = fp([1000, 1001, 999, -1000])
