@@ -294,25 +294,142 @@ def verify_sweep(args) -> dict:
             "decode_step_ms": round(float(np.median(steps[1:])), 3)}
 
 
+def embed_draft(target: "plamo_hip.Instance", draft: "plamo_hip.Instance", mix: float) -> int:
+    """The draft-weight policy of the speculative line: the target contains
+    the draft, and its own layers past the draft's are mixed in at `mix`.
+    Both models are tied (head = embedding) and share the layer layout rules
+    (sliding/global pattern, RoPE tables, attention scales). Before the
+    target's weights are uploaded:
+      - the embedding (= head) is the draft's in the first `hd` columns and
+        zero in the others;
+      - the first draft.count layers are the draft's layers and zero
+        elsewhere: the draft's query heads of KV group g become target query
+        heads tg*g.. (the target's group is larger), its KV heads the
+        target's first KV heads, its O, gate/up and down blocks the matching
+        sub-blocks; q/k norms are copied;
+      - every RMSNorm weight over the hidden dims is rescaled in the draft's
+        dims so that (w + offset) / rms over the wider vector equals the
+        draft's when the other dims are zero:
+        w_t = (w_d + offset) * sqrt(hd / ht) - offset (offsets: 1 pre-norms and
+        the final norm, 0.2 post-mixer, 0.0894 post-MLP; src/layer.s:51,
+        src/model.s:111);
+      - the target's later layers keep their own random weights, and their two
+        post-norms (which set the size of what a layer adds to the residual
+        stream, whatever its weights) are scaled to `mix` times their own:
+        w = mix * (w + offset) - offset.
+    With mix 0 the target computes the draft's function exactly (up to the
+    rounding of the rescaled norms); with mix 1 its later layers are ordinary
+    random layers. Returns the bytes written."""
+    tm, dm = target.model, draft.model
+    ht, hd, V = tm.hidden, dm.hidden, tm.vocab
+    assert dm.vocab == V and dm.count <= tm.count and hd <= ht
+
+    def view(ptr, *shape):
+        n = int(np.prod(shape))
+        return np.ctypeslib.as_array(ctypes.cast(ptr, plamo_hip.u16p), shape=(n,)).reshape(shape)
+
+    def f32(bits):
+        return (bits.astype(np.uint32) << 16).view(np.float32)
+
+    def bf16(x):
+        # Round to nearest even (finite inputs).
+        b = np.ascontiguousarray(x, np.float32).view(np.uint32)
+        return ((b + 0x7FFF + ((b >> 16) & 1)) >> 16).astype(np.uint16)
+
+    ratio = np.float32(np.sqrt(hd / ht))
+    written = 0
+
+    def put(dst, src):
+        nonlocal written
+        dst[...] = src
+        written += dst.nbytes
+
+    def norm(dst_ptr, src_ptr, offset):
+        dst, src = view(dst_ptr, ht), view(src_ptr, hd)
+        put(dst[:hd], bf16((f32(src) + np.float32(offset)) * ratio - np.float32(offset)))
+        put(dst[hd:], bf16(np.full(ht - hd, -offset, np.float32)))
+
+    emb = view(tm.embedding, V, ht)
+    put(emb[:, :hd], view(dm.embedding, V, hd))
+    put(emb[:, hd:], 0)
+    norm(tm.norm, dm.norm, 1.0)
+    for i in range(tm.count):
+        tl = tm.layers[i].contents
+        tx, tp = tl.mixer.contents, tl.mlp.contents
+        tq = tx.qkv.contents
+        if i >= dm.count:
+            for ptr, offset in ((tl.post, 0.2), (tp.post, 0.08944271909999159)):
+                w = view(ptr, ht)
+                put(w, bf16(np.float32(mix) * (f32(w) + np.float32(offset)) - np.float32(offset)))
+            continue
+        dl = dm.layers[i].contents
+        dx, dp = dl.mixer.contents, dl.mlp.contents
+        dq = dx.qkv.contents
+        d, tg, dg = tq.dim, tq.qh // tq.kh, dq.qh // dq.kh
+        assert dq.dim == d and dq.kh <= tq.kh and dg <= tg
+        norm(tl.pre, dl.pre, 1.0)
+        norm(tl.post, dl.post, 0.2)
+        norm(tp.pre, dp.pre, 1.0)
+        norm(tp.post, dp.post, 0.08944271909999159)
+        put(view(tq.qn, d), view(dq.qn, d))
+        put(view(tq.kn, d), view(dq.kn, d))
+        tw = view(tq.weight, tq.qh + 2 * tq.kh, d, ht)
+        dw = view(dq.weight, dq.qh + 2 * dq.kh, d, hd)
+        to = view(tx.weight, ht, tq.qh, d)
+        do = view(dx.weight, hd, dq.qh, d)
+        put(tw, 0)
+        put(to, 0)
+        for g in range(dq.kh):
+            for r in range(dg):
+                put(tw[tg * g + r, :, :hd], dw[dg * g + r])
+                put(to[:hd, tg * g + r, :], do[:, dg * g + r, :])
+            put(tw[tq.qh + g, :, :hd], dw[dq.qh + g])
+            put(tw[tq.qh + tq.kh + g, :, :hd], dw[dq.qh + dq.kh + g])
+        ti, di = tp.intermediate, dp.intermediate
+        tgu, dgu = view(tp.gu, 2 * ti, ht), view(dp.gu, 2 * di, hd)
+        tdn = view(tp.down, ht, ti)
+        put(tgu, 0)
+        put(tdn, 0)
+        put(tgu[:di, :hd], dgu[:di])
+        put(tgu[ti:ti + di, :hd], dgu[di:])
+        put(tdn[:hd, :di], view(dp.down, hd, di))
+    return written
+
+
 def speculative(args) -> dict:
     """the 31B-class model (C5, tied embedding/head) with
     the 0.8B-class model (C2 shape) as the in-process draft, 4 draft tokens
     per verify (a 5-token batched verify), a 455-token prompt and 128 greedy
     tokens through the engine's decode loop (runtime/engine.c:514-566,
-    plamo_hip_decode). Speculation must leave the tokens unchanged; with
-    unrelated random weights the draft is rarely right, so the acceptance
-    measured here is a property of the synthetic weights, and the per-round
-    component times are reported beside it."""
+    plamo_hip_decode). Speculation must leave the tokens unchanged.
+
+    Draft-weight policy: with unrelated random weights a draft is never right
+    (acceptance 0), so by default the draft is embedded in the target
+    (embed_draft) and the target's own later layers are mixed in at
+    --draft-mix. Random-weight models fall into short greedy cycles (the line
+    reports how many distinct tokens the target produced), which is what makes
+    the acceptance high when the two models share the cycle; the acceptance is
+    a property of this synthetic pair, and the per-round component times and
+    the rate projected at other acceptances are reported beside it."""
     tcfg = dict(plamo_hip.CONFIGS["c5"])
     tied = tcfg.pop("tied", 0)
     dcfg = dict(plamo_hip.CONFIGS["c2"])
     threads = host_threads()[0]
+    mix = args.draft_mix
     t0 = time.perf_counter()
     target = plamo_hip.Synthetic(**tcfg, tied=tied, seed=20261201, threads=threads)
-    source = plamo_hip.Synthetic(**dcfg, seed=20261202, threads=threads)
+    if mix is None:
+        source = plamo_hip.Synthetic(**dcfg, seed=20261202, threads=threads)
+    else:
+        source = plamo_hip.Synthetic(**dcfg, tied=1, seed=20261202, threads=threads)
     log(f"synthetic c5 ({target.mapping.bytes / 1e9:.1f} GB) and c2 draft "
         f"({source.mapping.bytes / 1e9:.1f} GB) in {time.perf_counter() - t0:.1f} s")
     inst, d_inst = target.instance(pinned=True), source.instance(pinned=True)
+    if mix is not None:
+        t0 = time.perf_counter()
+        written = embed_draft(inst, d_inst, mix)
+        log(f"draft embedded in the target ({written / 1e9:.2f} GB written, later layers "
+            f"mixed in at {mix}) in {time.perf_counter() - t0:.1f} s")
     be = plamo_hip.Backend(target)
     draft = plamo_hip.Draft(source, d_inst)
     block, max_tokens = 5, 128
@@ -376,12 +493,18 @@ def speculative(args) -> dict:
         "n_gpus": 1,
         "higher_is_better": True,
         "dtype": "fp32",
-        "data": "synthetic (seeded BF16 weights ~N(0,0.02); target and draft unrelated; "
-                "uniform random prompt ids)",
+        "data": ("synthetic (seeded BF16 weights ~N(0,0.02); target and draft unrelated; "
+                 "uniform random prompt ids)" if mix is None else
+                 "synthetic (seeded BF16 weights ~N(0,0.02); the tied c2-shape draft is the "
+                 "target's first 16 layers, the target's other 44 layers are its own, mixed "
+                 f"into the residual stream at {mix:g}; uniform random prompt ids)"),
+        "draft_policy": ("independent" if mix is None else
+                         f"embedded draft, later target layers mixed in at {mix:g}"),
         "config": {"workload": "c5 target (tied head) + c2-shape draft in process; 455-token "
                                "prompt, 128 greedy tokens, 4 draft tokens per verify",
                    "block": block, "max_tokens": max_tokens},
         "tokens_identical_to_plain": spec == plain,
+        "distinct_tokens": len(set(plain)),
         "completion_tokens": r.completion_tokens,
         "acceptance": round(r.accepted_tokens / max(1, r.proposed_tokens), 4),
         "verifies": r.speculative_batches,
@@ -423,6 +546,10 @@ def main() -> int:
     ap.add_argument("--verify", action="store_true",
                     help="time the C5 target's batched verify alone, per candidate count")
     ap.add_argument("--verify-tokens", default="1,2,3,4,5,6,8,16")
+    ap.add_argument("--draft-mix", type=float, default=0.3,
+                    help="--speculative: the draft is the target's first layers, and the "
+                         "target's later layers add this fraction of their usual share to the "
+                         "residual stream; negative: independent draft and target weights")
     ap.add_argument("--prefill-only", action="store_true",
                     help="measure TTFT for --ttft-sizes only (one JSON line, no decode)")
     ap.add_argument("--ttft-runs", type=int, default=12)
@@ -433,6 +560,8 @@ def main() -> int:
               file=sys.stderr)
         return 2
     if args.speculative:
+        if args.draft_mix is not None and args.draft_mix < 0:
+            args.draft_mix = None
         print(json.dumps(speculative(args)), flush=True)
         return 0
     if args.verify:

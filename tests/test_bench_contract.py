@@ -24,3 +24,44 @@ def test_help_lists_the_modes():
     assert r.returncode == 0
     for flag in ("--steps", "--warmup", "--speculative", "--verify", "--verify-tokens"):
         assert flag in r.stdout
+
+
+def test_embedded_draft_policy():
+    """The speculative line's draft-weight policy (bench.embed_draft) on the
+    CPU oracle at a small shape: with the target's later layers mixed in at 0
+    the target computes the draft's function, so their greedy choices agree
+    step for step (the rescaled norms are the only difference); at mix 1 the
+    later layers are ordinary random layers and the agreement is gone."""
+    import importlib.util
+
+    import numpy as np
+
+    import oracle_lib
+    import plamo_hip
+
+    spec = importlib.util.spec_from_file_location("bench", BENCH)
+    bench = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(bench)
+    agreement = {}
+    for mix in (0.0, 1.0):
+        d = plamo_hip.Synthetic(64, 4, 4, 2, 16, 128, 300, tied=1, seed=5, window=64,
+                                global_capacity=128, pattern=2)
+        t = plamo_hip.Synthetic(192, 15, 12, 4, 16, 384, 300, tied=1, seed=6, window=64,
+                                global_capacity=128, pattern=2)
+        di, ti = d.instance(), t.instance()
+        try:
+            assert bench.embed_draft(ti, di, mix) > 0
+            prompt = [int(x) for x in np.random.default_rng(1).integers(0, 300, 20)]
+            assert oracle_lib.prefill(di, prompt) and oracle_lib.prefill(ti, prompt)
+            same = 0
+            for _ in range(40):
+                a, b = int(np.argmax(di.logits())), int(np.argmax(ti.logits()))
+                same += a == b
+                assert oracle_lib.forward(di, b) and oracle_lib.forward(ti, b)
+            agreement[mix] = same
+        finally:
+            for x in (di, ti):
+                x.close()
+            d.close()
+            t.close()
+    assert agreement[0.0] >= 38 and agreement[1.0] <= 10, agreement
