@@ -78,6 +78,7 @@ struct GemmSplit {
     float *partial;
     uint32_t *counters;
     uint16_t *planes;
+    uint32_t xcd_group;  // nonzero: the M tiles of a weight tile share an XCD (see the kernel)
 };
 constexpr uint64_t kGemmPartialFloats = 16ull << 20;  // 64 MiB
 constexpr uint32_t kGemmCounters = 8192;

@@ -1037,19 +1037,35 @@ __global__ __launch_bounds__(256) void split_planes_kernel(const float *x, uint6
                                              pack_hi16(lo[4], lo[5]), pack_hi16(lo[6], lo[7])};
 }
 
-template <int WM, int WN>
-__global__ __launch_bounds__(256, WN > 2 ? 1 : 2) void gemm_split_kernel(GemmSplit g) {
-    constexpr int BM = 64 * WM, BN = 64 * WN;
+template <int WM, int WN, int GM = 2, int GN = 2>
+__global__ __launch_bounds__(64 * GM * GN, (WN > 2 || GM * GN > 4) ? 1 : 2) void gemm_split_kernel(
+    GemmSplit g) {
+    constexpr int NT = 64 * GM * GN;                             // threads: GM x GN waves
+    constexpr int BM = 32 * WM * GM, BN = 32 * WN * GN;
     constexpr int AG = 3 * BM * 4, WG = BN * 4, SG = AG + WG;  // granules per stage
-    constexpr int APT = AG / 256, WPT = WG / 256;               // granules per thread
+    constexpr int APT = AG / NT, WPT = WG / NT;                 // granules per thread
+    static_assert(AG % NT == 0 && WG % NT == 0, "whole granules per thread");
     extern __shared__ u32x4 lds[];                               // [2][SG]
     __shared__ int is_last;
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const uint32_t wm = wave >> 1, wn = wave & 1;
-    const uint32_t m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+    const uint32_t wm = wave / GN, wn = wave % GN;
+    // Tile of this block. The dispatcher hands blocks to the 8 XCDs in turn
+    // (linear block id modulo 8), each with its own L2. With xcd_group, the
+    // M tiles of one (weight tile, K split) get consecutive turns on one XCD,
+    // so the weight tile crosses HBM once and the other M tiles read it from
+    // that XCD's L2 (without it, every M tile re-streams the whole matrix).
+    uint32_t bn = blockIdx.x, bm = blockIdx.y, bz = blockIdx.z;
+    if (g.xcd_group) {
+        const uint32_t lin = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
+        const uint32_t slot = lin / 8, group = slot / gridDim.y * 8 + lin % 8;
+        bm = slot % gridDim.y;
+        bn = group % gridDim.x;
+        bz = group / gridDim.x;
+    }
+    const uint32_t m0 = bm * BM, n0 = bn * BN;
     const uint32_t kper = g.k / g.splits;
-    const uint32_t kbeg = blockIdx.z * kper, nst = kper / kSplitBK;
-    const uint32_t first = blockIdx.x % nst;  // rotation of this block's stages
+    const uint32_t kbeg = bz * kper, nst = kper / kSplitBK;
+    const uint32_t first = bn % nst;  // rotation of this block's stages
     const uint64_t stage_elems = 3ull * g.tp * kSplitBK;  // planes of one stage
 
     // Staging: granule G = threadIdx + 256 i of the stage; A granules first.
@@ -1057,7 +1073,7 @@ __global__ __launch_bounds__(256, WN > 2 ? 1 : 2) void gemm_split_kernel(GemmSpl
     uint32_t adst[APT];
 #pragma unroll
     for (int i = 0; i < APT; ++i) {
-        const uint32_t G = threadIdx.x + 256 * i, R = G / 4, q = G % 4;
+        const uint32_t G = threadIdx.x + NT * i, R = G / 4, q = G % 4;
         const uint32_t p = R / BM, r = R % BM;
         asrc[i] = g.planes + ((uint64_t)p * g.tp + m0 + r) * kSplitBK + 8 * q;
         adst[i] = R * 4 + swizzle(R, q);
@@ -1066,7 +1082,7 @@ __global__ __launch_bounds__(256, WN > 2 ? 1 : 2) void gemm_split_kernel(GemmSpl
     uint32_t wdst[WPT];
 #pragma unroll
     for (int i = 0; i < WPT; ++i) {
-        const uint32_t G = threadIdx.x + 256 * i, r = G / 4, q = G % 4;
+        const uint32_t G = threadIdx.x + NT * i, r = G / 4, q = G % 4;
         wsrc[i] = g.w + (uint64_t)min(n0 + r, g.n - 1) * g.k + 8 * q;
         wdst[i] = AG + r * 4 + swizzle(r, q);
     }
@@ -1155,11 +1171,11 @@ __global__ __launch_bounds__(256, WN > 2 ? 1 : 2) void gemm_split_kernel(GemmSpl
 
     // D layout of v_mfma_f32_32x32x16: value v of lane l is row
     // 8 (v / 4) + 4 (l / 32) + v % 4, column l % 32 of the 32 x 32 tile.
-    const uint32_t tile = blockIdx.y * gridDim.x + blockIdx.x;
+    const uint32_t tile = bm * gridDim.x + bn;
     const uint32_t tiles = gridDim.x * gridDim.y;
     if (g.splits > 1) {
         // Partial tile, laid out [split][tile][wave][i][j][v][lane] (coalesced).
-        float *part = g.partial + ((uint64_t)blockIdx.z * tiles + tile) * (BM * BN);
+        float *part = g.partial + ((uint64_t)bz * tiles + tile) * (BM * BN);
 #pragma unroll
         for (int i = 0; i < WM; ++i)
 #pragma unroll
@@ -1211,37 +1227,42 @@ __global__ __launch_bounds__(256, WN > 2 ? 1 : 2) void gemm_split_kernel(GemmSpl
         }
 }
 
-template <int WM, int WN>
+template <int WM, int WN, int GM = 2, int GN = 2>
 static hipError_t gemm_split_variant(hipStream_t stream, GemmSplit g, const GemmWorkspace &ws) {
-    constexpr uint32_t BM = 64 * WM, BN = 64 * WN;
+    constexpr uint32_t BM = 32 * WM * GM, BN = 32 * WN * GN;
     const uint32_t nt = (g.n + BN - 1) / BN, mt = (g.t + BM - 1) / BM;
     const uint32_t tiles = nt * mt, stages = g.k / kSplitBK;
     g.tp = mt * BM;
     if ((uint64_t)3 * g.tp * g.k > ws.plane_elems) return hipErrorInvalidValue;
-    // Two blocks per CU: aim for 512 blocks, each split at least four stages.
+    // About one block per CU (measured against 128, 384 and 512: each K split
+    // adds a partial tile to write and sum), each split at least four stages.
     uint32_t splits = 1;
-    while (tiles * splits < 512 && stages % (2 * splits) == 0 && stages / (2 * splits) >= 4 &&
+    while (tiles * splits < 256 && stages % (2 * splits) == 0 && stages / (2 * splits) >= 4 &&
            splits < 8)
         splits *= 2;
-    if (splits > 1 && ((uint64_t)splits * tiles * BM * BN > ws.partial_floats ||
-                       tiles > ws.counters))
-        splits = 1;
+    // Fewer splits while the partial tiles exceed the workspace (not straight
+    // to one: a 96-tile projection would then leave most CUs idle).
+    while (splits > 1 && ((uint64_t)splits * tiles * BM * BN > ws.partial_floats ||
+                          tiles > ws.counters))
+        splits /= 2;
     g.splits = splits;
     g.partial = ws.partial;
     g.counters = ws.counter_base;
     g.planes = ws.planes;
+    // Grouping needs whole turns of the 8 XCDs: (weight tiles x splits) % 8 == 0.
+    g.xcd_group = mt > 1 && (nt * splits) % 8 == 0;
     const uint64_t elems = (uint64_t)g.tp * g.k;
     split_planes_kernel<<<(unsigned)((elems / 8 + 255) / 256), 256, 0, stream>>>(
         g.x, g.ldx, g.t, g.tp, g.k, ws.planes);
     const size_t lds = 2 * (size_t)(3 * BM * 4 + BN * 4) * sizeof(u32x4);
     static bool attr = false;
     if (!attr) {
-        hipError_t e = hipFuncSetAttribute((const void *)gemm_split_kernel<WM, WN>,
+        hipError_t e = hipFuncSetAttribute((const void *)gemm_split_kernel<WM, WN, GM, GN>,
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (e != hipSuccess) return e;
         attr = true;
     }
-    gemm_split_kernel<WM, WN><<<dim3(nt, mt, splits), 256, lds, stream>>>(g);
+    gemm_split_kernel<WM, WN, GM, GN><<<dim3(nt, mt, splits), 64 * GM * GN, lds, stream>>>(g);
     return hipGetLastError();
 }
 
@@ -1485,11 +1506,11 @@ struct TokenGemv {
 constexpr uint32_t kTokenMax = 5;
 constexpr uint32_t kTokenU = 8;
 constexpr uint32_t kTokenKC = 2;
-constexpr uint32_t kTokenXBytes = 64 * 1024;    // X slice per block
-constexpr uint32_t kTokenLdsBytes = 80 * 1024;  // X slice + staged sums: two blocks per CU
+constexpr uint32_t kTokenXBytes = 128 * 1024;    // X slice per block
+constexpr uint32_t kTokenLdsBytes = 156 * 1024;  // X slice + staged sums: one block per CU
 
 template <int T>
-__global__ __launch_bounds__(256, 2) void token_gemv_kernel(TokenGemv g) {
+__global__ __launch_bounds__(256, 1) void token_gemv_kernel(TokenGemv g) {
     static_assert(T >= 1 && T <= (int)kTokenMax, "token count the plan admits");
     constexpr uint32_t U = kTokenU, KC = kTokenKC, UT = U * T, H = U / 2;
     extern __shared__ float tg_lds[];
@@ -1677,8 +1698,10 @@ struct TokenPlan {
 };
 
 // Slices: the fewest (dividing the 512-column chunks) whose X slice fits
-// kTokenXBytes. Row groups: two blocks per CU over all slices, fewer when
-// rows run out, more when the staged sums would not fit the LDS budget.
+// kTokenXBytes (a 6144-wide projection of 5 tokens needs none). Row groups:
+// one block per CU over all slices, fewer when rows run out, more when the
+// staged sums would not fit the LDS budget. (Two blocks per CU with 64 KB
+// slices: verify(5) at C5 17.7 against 17.0 ms.)
 static bool token_plan(uint64_t rows, uint64_t cols, uint64_t tokens, uint64_t half,
                        uint32_t cus, TokenPlan &p) {
     if (!tokens || tokens > kTokenMax || !rows || cols % 512 || cols > (1u << 30) ||
@@ -1691,7 +1714,7 @@ static bool token_plan(uint64_t rows, uint64_t cols, uint64_t tokens, uint64_t h
     if (!slices) return false;
     const uint64_t ks = cols / slices;
     const uint64_t units = half ? half / (kTokenU / 2) : (rows + kTokenU - 1) / kTokenU;
-    uint64_t blocks = std::max<uint64_t>(1, 2ull * std::max<uint32_t>(cus, 1) / slices);
+    uint64_t blocks = std::max<uint64_t>(1, 1ull * std::max<uint32_t>(cus, 1) / slices);
     blocks = std::min<uint64_t>(blocks, (units + 3) / 4);
     const uint64_t budget = kTokenLdsBytes / 4 / tokens;  // floats per block per token
     if (budget <= ks) return false;
@@ -1812,13 +1835,14 @@ hipError_t launch_gemm(hipStream_t stream, const float *x, uint64_t x_stride, co
         g.t = (uint32_t)tokens;
         g.y = y;
         g.ldy = y_stride;
-        // Wide tiles (64 x 128 per wave) when there are enough of them: fewer
-        // LDS bytes per MFMA and half the re-reads of X.
+        // Wide tiles (128 tokens x 256 rows per block, as 8 waves of 64 x 64:
+        // two waves per SIMD) when there are enough of them: fewer LDS bytes
+        // per MFMA and half the re-reads of X.
         const bool wide = (rows + 255) / 256 * ((tokens + 127) / 128) >= 64;
         if (tokens <= 64)
             return wide ? gemm_split_variant<1, 4>(stream, g, *ws)
                         : gemm_split_variant<1, 2>(stream, g, *ws);
-        return wide ? gemm_split_variant<2, 4>(stream, g, *ws)
+        return wide ? gemm_split_variant<2, 2, 2, 4>(stream, g, *ws)
                     : gemm_split_variant<2, 2>(stream, g, *ws);
     }
     if (tokens <= 16) return gemm_variant<16, 64>(stream, x, x_stride, w, rows, cols, tokens, y, y_stride);
@@ -2816,23 +2840,52 @@ __global__ __launch_bounds__(kThreads) void prompt_attention_kernel(PromptAttent
 // One block per (token, head): rescales each split's record to the common
 // maximum and normalizes by the combined sum. Splits with no visible key
 // carry a -inf maximum and contribute nothing.
+// One block per (token, head). The splits' maxima and sums are loaded at once
+// (one lane per split) and their factors exp(m_z - m) staged in LDS; then the
+// sum of weights and each output column are accumulated over the splits in
+// split order, skipping splits that saw no key (maximum -inf), as a plain
+// sequential loop over the records would.
+constexpr uint32_t kMergeSplits = 64;
 __global__ __launch_bounds__(128) void attention_merge_kernel(const float *partial,
                                                               uint32_t splits, uint64_t stride,
                                                               uint32_t dim, float *out) {
+    __shared__ float fz[kMergeSplits], lz[kMergeSplits];
+    __shared__ uint32_t live[kMergeSplits];
+    __shared__ float total;
     const float *p = partial + (uint64_t)blockIdx.x * (dim + 2);
-    float m = -__builtin_inff();
-    for (uint32_t z = 0; z < splits; ++z) m = fmaxf(m, p[z * stride + dim]);
-    float l = 0.0f;
-    for (uint32_t z = 0; z < splits; ++z) {
-        const float mz = p[z * stride + dim];
-        if (mz != -__builtin_inff()) l += p[z * stride + dim + 1] * plamo_exp(mz - m);
+    const uint32_t lane = threadIdx.x;
+    if (lane < 64) {
+        const bool in = lane < splits;
+        const float mz = in ? p[lane * stride + dim] : -__builtin_inff();
+        const float sz = in ? p[lane * stride + dim + 1] : 0.0f;
+        const float m = wave_max(mz);
+        const bool on = mz != -__builtin_inff();
+        fz[lane] = on ? plamo_exp(mz - m) : 0.0f;
+        lz[lane] = sz;
+        live[lane] = on;
     }
-    for (uint32_t d = threadIdx.x; d < dim; d += 128) {
+    __syncthreads();
+    if (lane == 0) {
+        float l = 0.0f;
+        for (uint32_t z = 0; z < splits; ++z)
+            if (live[z]) l += lz[z] * fz[z];
+        total = l;
+    }
+    __syncthreads();
+    const float l = total;
+    for (uint32_t d = lane; d < dim; d += 128) {
         float acc = 0.0f;
-        for (uint32_t z = 0; z < splits; ++z) {
-            const float mz = p[z * stride + dim];
-            if (mz != -__builtin_inff()) acc += p[z * stride + d] * plamo_exp(mz - m);
+        uint32_t z = 0;
+        for (; z + 8 <= splits; z += 8) {
+            float v[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) v[j] = p[(z + j) * stride + d];
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+                if (live[z + j]) acc += v[j] * fz[z + j];
         }
+        for (; z < splits; ++z)
+            if (live[z]) acc += p[z * stride + d] * fz[z];
         out[(uint64_t)blockIdx.x * dim + d] = acc / l;
     }
 }
