@@ -37,10 +37,11 @@ namespace {
 constexpr float kAttentionOffset = 0.2f;                  // src/layer.s:51
 constexpr float kMlpOffset = 0.08944271909999159f;        // src/model.s:111
 // Device KV rows allocated per layer at first, doubled on demand. Small on
-// purpose: the decode attention launch has one block per KV head per 64
-// allocated rows, and the blocks past the current row count still pass
-// through the CU slots ahead of the O-projection blocks of the same launch.
-constexpr uint64_t kInitialRows = 512;
+// purpose: the decode attention launch has one block per KV head per 32
+// allocated rows (up to 256 rows; per 64 beyond), and the blocks past the
+// current row count still pass through the CU slots ahead of the
+// O-projection blocks of the same launch.
+constexpr uint64_t kInitialRows = 256;
 constexpr uint64_t kMaxPrompt = 4096;                     // runtime/metal_model.m:540
 
 struct Range {

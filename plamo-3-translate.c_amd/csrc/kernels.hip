@@ -2074,13 +2074,13 @@ hipError_t launch_qkv_post(hipStream_t stream, const QkvPost &a) {
 // Decode attention for one KV head group per block, with the reference's
 // softmax (tests/attention_reference.s:8-112: scores as FMA chains times
 // 1/sqrt(d), the maximum over all rows, exp, sum, weighted value sum).
-// Blocks of 8 waves take up to kRowsPerBlock rows; longer contexts are split
-// across blocks whose partials (max, sum, weighted values) the last block of
-// the KV head merges.
+// Blocks of 8 waves take up to ROWS rows; longer contexts are split across
+// blocks whose partials (max, sum, weighted values) the last block of the KV
+// head merges.
 //
 // Phase 0: every load goes out at once, none waiting for the row count: the
 // query heads, the new key/value and their norm weights, and the block's
-// fixed tile of 64 cached K and V rows (rows [64 * split, 64 * split + 64),
+// fixed tile of ROWS cached K and V rows (rows [ROWS * split, ROWS * split + ROWS),
 // clamped to the allocation; rows at or past the count are masked once it
 // has arrived). The rotation of the step's position is evaluated in FP64 as
 // the table's rows are (no table lookup after the count). The query heads are
@@ -2092,17 +2092,24 @@ hipError_t launch_qkv_post(hipStream_t stream, const QkvPost &a) {
 // Phase 3: values. Lanes own DIM/64 adjacent columns; each wave accumulates
 // its rows' weighted values, the waves are summed in LDS.
 constexpr uint32_t kAttnWaves = 8, kAttnThreads = 64 * kAttnWaves;
-// One pass of 8 rows per wave: a block loads at most 64 K and V rows, so a
-// context is spread over many CUs (one CU's load path is the limit otherwise).
-constexpr uint32_t kRowsPerBlock = 64;
+// Rows per block, one pass per wave: a block loads at most ROWS K and V rows,
+// so a context is spread over many CUs (one CU's load path is the limit
+// otherwise). Up to kShortAlloc allocated rows, kShortRows per block (more
+// blocks in flight for a short context); beyond, kRowsPerBlock (fewer partials
+// to merge for a long one).
+constexpr uint32_t kRowsPerBlock = 64, kShortRows = 32, kShortAlloc = 256;
+
+__host__ __device__ constexpr uint32_t attention_rows(uint64_t rows) {
+    return rows <= kShortAlloc ? kShortRows : kRowsPerBlock;
+}
 
 // One attention block (KV head kvh, row split `split`). With `done`, the block
 // that completes a KV head's output writes it through to the coherence point
 // and counts the head in *done (the fused O projection waits on it).
-template <int DIM, int G, int W>
+template <int DIM, int G, int W, int ROWS>
 __device__ __forceinline__ void attention_block(const DecodeAttention &a, uint32_t kvh,
                                                 uint32_t split, uint32_t *done) {
-    constexpr uint32_t RW = kRowsPerBlock / W;  // rows per wave
+    constexpr uint32_t RW = ROWS / W;  // rows per wave
     constexpr uint32_t P = W * RW;              // rows per pass (one block)
     constexpr int HPW = (G + W - 1) / W;        // query heads per wave
     constexpr int PL = DIM / 64;             // value columns per lane
@@ -2118,8 +2125,8 @@ __device__ __forceinline__ void attention_block(const DecodeAttention &a, uint32
     float *qs = smem;                            // [G][DIM]
     float *knew = qs + G * DIM;                  // [DIM] rotated new key
     float *vnew = knew + DIM;                    // [DIM]
-    float *sc = vnew + DIM;                      // [kRowsPerBlock + 1][G]
-    float *wpart = sc + (kRowsPerBlock + 1) * G; // [W][G][DIM]
+    float *sc = vnew + DIM;                      // [ROWS + 1][G]
+    float *wpart = sc + (ROWS + 1) * G;          // [W][G][DIM]
 
     // The step's query/key/value heads: wave w normalizes query heads w,
     // w + W, ..., the last wave the new key; lane j < DIM/2 holds elements j
@@ -2154,7 +2161,7 @@ __device__ __forceinline__ void attention_block(const DecodeAttention &a, uint32
     const float freq = a.freq[hj];
 
     const uint32_t count = a.params->count[a.layer];
-    const uint32_t lo = split * kRowsPerBlock;
+    const uint32_t lo = split * ROWS;
     const uint32_t last_row = a.rows - 1;
     const float *kbase = a.k_rot + (uint64_t)kvh * DIM;
     const float *vbase = a.v + (uint64_t)kvh * DIM;
@@ -2205,8 +2212,8 @@ __device__ __forceinline__ void attention_block(const DecodeAttention &a, uint32
     // scored from LDS); tiles past them have nothing to do.
     const uint32_t n = count + 1;
     if (lo >= n) return;
-    const uint32_t splits = (n + kRowsPerBlock - 1) / kRowsPerBlock;
-    const uint32_t hi = lo + kRowsPerBlock < n ? lo + kRowsPerBlock : n;
+    const uint32_t splits = (n + ROWS - 1) / ROWS;
+    const uint32_t hi = lo + ROWS < n ? lo + ROWS : n;
     const bool owner = count >= lo && count < hi;
     const uint32_t hr = hi < count ? hi : count;  // cached rows of this block
     float rc, rs;
@@ -2484,9 +2491,9 @@ __device__ __forceinline__ void attention_block(const DecodeAttention &a, uint32
     if (done) arrive_last(done, 0xffffffffu, &is_last);
 }
 
-template <int DIM, int G>
+template <int DIM, int G, int ROWS>
 __global__ __launch_bounds__(kAttnThreads) void decode_attention_kernel(DecodeAttention a) {
-    attention_block<DIM, G, kAttnWaves>(a, blockIdx.x, blockIdx.y, nullptr);
+    attention_block<DIM, G, kAttnWaves, ROWS>(a, blockIdx.x, blockIdx.y, nullptr);
 }
 
 // Attention fused with the output projection (src/mixer.s:60-80: O = W_o .
@@ -2561,11 +2568,12 @@ __device__ __forceinline__ void oproj_block(const AttentionO &f, uint32_t ob) {
     if (!ok && lane == 0) atomicOr(f.error, 1u);
 }
 
-template <int DIM, int G, int KC>
+template <int DIM, int G, int KC, int ROWS>
 __global__ __launch_bounds__(kAttnThreads) void attention_o_kernel(AttentionO f) {
     const uint32_t attention_blocks = f.a.kh * f.a.splits;
     if (blockIdx.x < attention_blocks)
-        attention_block<DIM, G, kAttnWaves>(f.a, blockIdx.x % f.a.kh, blockIdx.x / f.a.kh, f.done);
+        attention_block<DIM, G, kAttnWaves, ROWS>(f.a, blockIdx.x % f.a.kh, blockIdx.x / f.a.kh,
+                                                  f.done);
     else
         oproj_block<KC>(f, blockIdx.x - attention_blocks);
 }
@@ -2576,24 +2584,35 @@ bool decode_attention_supported(uint32_t dim, uint32_t group) {
 }
 
 uint32_t decode_attention_splits(uint64_t rows) {
-    return (uint32_t)((rows + kRowsPerBlock - 1) / kRowsPerBlock);
+    const uint32_t per = attention_rows(rows);
+    return (uint32_t)((rows + per - 1) / per);
 }
 
-static size_t decode_attention_lds(uint32_t dim, uint32_t group, uint32_t waves = kAttnWaves) {
-    return (group * dim + 2 * dim + (kRowsPerBlock + 1) * group + waves * group * dim) *
+static size_t decode_attention_lds(uint32_t dim, uint32_t group, uint32_t rows,
+                                   uint32_t waves = kAttnWaves) {
+    return (group * dim + 2 * dim + (rows + 1) * group + waves * group * dim) *
            sizeof(float);
+}
+
+// Rows per block follow the allocated rows (attention_rows); a.splits is
+// decode_attention_splits of the same count.
+template <int DIM, int G, int ROWS>
+static hipError_t decode_attention_rows(hipStream_t stream, const DecodeAttention &a) {
+    size_t lds = decode_attention_lds(DIM, G, ROWS);
+    if (lds > 65536) {
+        hipError_t e = hipFuncSetAttribute((const void *)decode_attention_kernel<DIM, G, ROWS>,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) return e;
+    }
+    decode_attention_kernel<DIM, G, ROWS><<<dim3(a.kh, a.splits), kAttnThreads, lds, stream>>>(a);
+    return hipGetLastError();
 }
 
 template <int DIM, int G>
 static hipError_t decode_attention_variant(hipStream_t stream, const DecodeAttention &a) {
-    size_t lds = decode_attention_lds(DIM, G);
-    if (lds > 65536) {
-        hipError_t e = hipFuncSetAttribute((const void *)decode_attention_kernel<DIM, G>,
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-        if (e != hipSuccess) return e;
-    }
-    decode_attention_kernel<DIM, G><<<dim3(a.kh, a.splits), kAttnThreads, lds, stream>>>(a);
-    return hipGetLastError();
+    return attention_rows(a.rows) == kShortRows
+               ? decode_attention_rows<DIM, G, kShortRows>(stream, a)
+               : decode_attention_rows<DIM, G, kRowsPerBlock>(stream, a);
 }
 
 template <int DIM>
@@ -2607,24 +2626,31 @@ static hipError_t decode_attention_dim(hipStream_t stream, const DecodeAttention
     }
 }
 
-template <int DIM, int G, int KC>
+template <int DIM, int G, int KC, int ROWS>
 static hipError_t attention_o_variant(hipStream_t stream, const AttentionO &f) {
-    const size_t lds = std::max(decode_attention_lds(DIM, G), kAttentionOLds);
-    hipError_t e = hipFuncSetAttribute((const void *)attention_o_kernel<DIM, G, KC>,
+    const size_t lds = std::max(decode_attention_lds(DIM, G, ROWS), kAttentionOLds);
+    hipError_t e = hipFuncSetAttribute((const void *)attention_o_kernel<DIM, G, KC, ROWS>,
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return e;
     const uint32_t oblocks = (f.rows + kORows * kAttnWaves - 1) / (kORows * kAttnWaves);
-    attention_o_kernel<DIM, G, KC>
+    attention_o_kernel<DIM, G, KC, ROWS>
         <<<f.a.kh * f.a.splits + oblocks, kAttnThreads, lds, stream>>>(f);
     return hipGetLastError();
+}
+
+template <int DIM, int G, int KC>
+static hipError_t attention_o_rows(hipStream_t stream, const AttentionO &f) {
+    return attention_rows(f.a.rows) == kShortRows
+               ? attention_o_variant<DIM, G, KC, kShortRows>(stream, f)
+               : attention_o_variant<DIM, G, KC, kRowsPerBlock>(stream, f);
 }
 
 template <int DIM, int G>
 static hipError_t attention_o_cols(hipStream_t stream, const AttentionO &f) {
     switch (f.cols / 512) {
-    case 4: return attention_o_variant<DIM, G, 4>(stream, f);
-    case 8: return attention_o_variant<DIM, G, 8>(stream, f);
-    default: return attention_o_variant<DIM, G, 12>(stream, f);
+    case 4: return attention_o_rows<DIM, G, 4>(stream, f);
+    case 8: return attention_o_rows<DIM, G, 8>(stream, f);
+    default: return attention_o_rows<DIM, G, 12>(stream, f);
     }
 }
 
