@@ -148,6 +148,10 @@ struct plamo_metal {
 
     hipGraphExec_t graph = nullptr;
     uint64_t epoch = 1, graph_epoch = 0;
+    // The same step for contexts below kDecodeShortRows rows in every layer,
+    // with the attention's view of the allocation capped there.
+    hipGraphExec_t graph_short = nullptr;
+    uint64_t graph_short_epoch = 0;
     std::vector<void *> allocations;
 };
 
@@ -361,10 +365,11 @@ bool alloc_verify(plamo_metal *m, uint64_t L, uint64_t h, uint64_t V) {
 }
 
 void release_model(plamo_metal *m) {
-    if (m->graph) {
-        (void)hipGraphExecDestroy(m->graph);
-        m->graph = nullptr;
-    }
+    for (hipGraphExec_t *g : {&m->graph, &m->graph_short})
+        if (*g) {
+            (void)hipGraphExecDestroy(*g);
+            *g = nullptr;
+        }
     for (Layer &l : m->layers) {
         dev_free(m, l.norms);
         dev_free(m, l.k);
@@ -749,6 +754,10 @@ struct DecodePlan {
     std::vector<char> stale, shift;
     bool special = false;
     bool direct = false;  // host arrays written in place by the step itself
+    // Nonzero: every layer's rows stay below this count for the step, and the
+    // decode attention sees at most this many allocated rows (its
+    // short-context blocks).
+    uint32_t row_cap = 0;
 };
 
 // Enqueues one decode step: embedding, every layer, final norm + head, and the
@@ -793,7 +802,7 @@ int encode_decode(plamo_metal *m, struct model *model, const DecodePlan &plan, i
             da.freq = rope.freq_dev;
             memcpy(&da.rope_scale, &rope.scale_bits, 4);
             da.k_raw = d.k;
-            da.rows = (uint32_t)d.rows;
+            da.rows = (uint32_t)(plan.row_cap ? std::min<uint64_t>(d.rows, plan.row_cap) : d.rows);
             da.v = d.v;
             da.k_rot = d.rot;
             da.stage = plan.direct ? nullptr : layer_stage;
@@ -810,7 +819,7 @@ int encode_decode(plamo_metal *m, struct model *model, const DecodePlan &plan, i
             da.qh = d.qh;
             da.kh = d.kh;
             da.dim = d.dim;
-            da.splits = decode_attention_splits(d.rows);
+            da.splits = decode_attention_splits(da.rows);
             return da;
         };
         HIP_TRY(m, launch_gemv(s, d.qkv, qkv_rows, h, p1, m->qkv, 0, blocks));
@@ -1208,30 +1217,36 @@ int plamo_metal_forward(struct plamo_metal *m, struct model *model, uint64_t tok
     m->params_host->tokens = 1;
     *m->status_host = 0;
     plan.direct = m->host_direct && !plan.special;
+    bool short_ctx = true;
+    for (uint64_t i = 0; i < L && short_ctx; ++i)
+        short_ctx = model->layers[i]->mixer->cache->count + 1 <= kDecodeShortRows;
+    plan.row_cap = short_ctx ? kDecodeShortRows : 0;
     int dispatches = 0;
     begin_timing(m);
     if (plan.special) {
         if (!encode_decode(m, model, plan, &dispatches)) return fail(m);
     } else {
-        if (!m->graph || m->graph_epoch != m->epoch) {
-            if (m->graph) (void)hipGraphExecDestroy(m->graph);
-            m->graph = nullptr;
+        hipGraphExec_t &g = short_ctx ? m->graph_short : m->graph;
+        uint64_t &g_epoch = short_ctx ? m->graph_short_epoch : m->graph_epoch;
+        if (!g || g_epoch != m->epoch) {
+            if (g) (void)hipGraphExecDestroy(g);
+            g = nullptr;
             hipGraph_t graph = nullptr;
             int ok = hipStreamBeginCapture(m->stream, hipStreamCaptureModeThreadLocal) == hipSuccess;
             int encoded = ok && encode_decode(m, model, plan, &dispatches);
             ok = hipStreamEndCapture(m->stream, &graph) == hipSuccess && encoded && graph;
-            ok = ok && hipGraphInstantiate(&m->graph, graph, nullptr, nullptr, 0) == hipSuccess;
+            ok = ok && hipGraphInstantiate(&g, graph, nullptr, nullptr, 0) == hipSuccess;
             if (graph) (void)hipGraphDestroy(graph);
             if (!ok) {
                 (void)hipGetLastError();
-                m->graph = nullptr;
+                g = nullptr;
                 problem(m, "cannot capture the decode graph");
                 return fail(m);
             }
-            m->graph_epoch = m->epoch;
+            g_epoch = m->epoch;
         }
         dispatches = (int)(2 + 5 * L);
-        if (hipGraphLaunch(m->graph, m->stream) != hipSuccess) {
+        if (hipGraphLaunch(g, m->stream) != hipSuccess) {
             (void)hipGetLastError();
             problem(m, "decode graph launch failed");
             return fail(m);

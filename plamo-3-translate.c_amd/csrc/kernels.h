@@ -172,6 +172,10 @@ hipError_t launch_attention_o(hipStream_t, const AttentionO &);
 bool attention_o_supported(uint32_t dim, uint32_t group, uint64_t cols);
 // Blocks per KV head that cover `rows` cache rows (DecodeAttention::splits
 // must be at least this for the largest row count of the launch).
+// Allocated rows up to which the decode attention uses its short-context
+// blocks (32 rows each); a decode step whose rows all stay below it may cap
+// the attention's view of the allocation here.
+constexpr uint32_t kDecodeShortRows = 256;
 uint32_t decode_attention_splits(uint64_t rows);
 
 // General causal attention for `tokens` query rows. Key j of query t is the

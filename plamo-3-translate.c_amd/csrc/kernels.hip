@@ -2097,7 +2097,7 @@ constexpr uint32_t kAttnWaves = 8, kAttnThreads = 64 * kAttnWaves;
 // otherwise). Up to kShortAlloc allocated rows, kShortRows per block (more
 // blocks in flight for a short context); beyond, kRowsPerBlock (fewer partials
 // to merge for a long one).
-constexpr uint32_t kRowsPerBlock = 64, kShortRows = 32, kShortAlloc = 256;
+constexpr uint32_t kRowsPerBlock = 64, kShortRows = 32, kShortAlloc = kDecodeShortRows;
 
 __host__ __device__ constexpr uint32_t attention_rows(uint64_t rows) {
     return rows <= kShortAlloc ? kShortRows : kRowsPerBlock;

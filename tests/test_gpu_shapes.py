@@ -245,3 +245,39 @@ def test_long_context_split_attention():
         run_pair(syn, steps=3, prompt=None, fill=3000)
     finally:
         syn.close()
+
+
+@pytest.mark.parametrize("pinned", [False, True])
+def test_short_context_graph_boundary(pinned):
+    # Below 256 rows in every layer a decode step runs the short-context graph
+    # (32-row attention blocks over at most 256 allocated rows); the step whose
+    # count reaches 256 switches to the general graph. 250 -> 262 crosses it,
+    # with the allocation grown to 512 rows first (a longer prompt earlier in
+    # the request), as the bench's decode runs after its 455-token prompts.
+    syn = plamo_hip.Synthetic(512, 2, 8, 2, 128, 1024, 500, window=4096, global_capacity=8192,
+                              pattern=2, embedding_std=1.0, seed=405)
+    try:
+        run_pair(syn, steps=12, prompt=None, fill=250, pinned=pinned)
+        gpu, cpu = syn.instance(pinned=pinned), syn.instance()
+        be = plamo_hip.Backend(syn)
+        try:
+            prompt = [(j * 13 + 5) % 500 for j in range(300)]
+            assert be.prefill(gpu, prompt) == 1  # allocation grows past 256 rows
+            gpu.reset()
+            cpu.reset()
+            assert be.prefill(gpu, prompt[:200]) == 1
+            assert oracle_lib.prefill(cpu, prompt[:200])
+            token = int(np.argmax(cpu.logits()))
+            for step in range(60):
+                assert be.forward(gpu, token) == 1
+                assert oracle_lib.forward(cpu, token)
+                compare(gpu, cpu)
+                token = int(np.argmax(cpu.logits()))
+            info = be.info()
+            assert info.errors == 0 and info.cpu_fallbacks == 0, info.note.decode()
+        finally:
+            be.close()
+            gpu.close()
+            cpu.close()
+    finally:
+        syn.close()
