@@ -2508,10 +2508,12 @@ __global__ __launch_bounds__(kAttnThreads) void decode_attention_kernel(DecodeAt
 // O rows per wave of the fused kernel, and the LDS every block of it claims:
 // more than half of a CU's 160 KiB, so a CU holds one block. With the KV
 // rows allocated in small steps the launch (64 attention blocks at C4 below
-// 512 rows plus 171 O blocks) then fits the 256 CUs at once: every O block
-// requests its weights at the start, and no O block's 128 KB of weight loads
+// 256 rows plus 128 O blocks) then fits the 256 CUs at once: every O block
+// requests its weights at the start, and no O block's 256 KB of weight loads
 // shares a CU's load path with an attention block's latency-bound loads.
-constexpr int kORows = 3;
+// (Rows per wave, C4 ms per step: 2: 3.114, 3: 3.089, 4: 3.053, 5: 3.060,
+// 6: 3.114.)
+constexpr int kORows = 4;
 constexpr size_t kAttentionOLds = 96 * 1024;
 
 template <int KC>
