@@ -17,6 +17,7 @@
 #include <hip/hip_runtime.h>
 #include <stdarg.h>
 #include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include <algorithm>
@@ -126,6 +127,11 @@ struct plamo_metal {
     // When every host array a step updates is pinned and device-visible, the
     // graph writes them in place (no host-side mirror copies).
     bool host_direct = false;
+    // PLAMO_HIP_EAGER_DECODE=1 at open: every decode step launches its kernels
+    // one by one instead of replaying the captured graph (same kernels, same
+    // arguments). For profilers that trace kernel launches but not graph
+    // replays.
+    bool eager_decode = false;
     float *host_state = nullptr, *host_norm = nullptr;
     // The device's error word of the last call, copied by the call's last
     // kernel (or a copy) into pinned host memory; status_dev is its device view.
@@ -1101,6 +1107,8 @@ struct plamo_metal *plamo_metal_open(const struct plamo_metal_config *config, ch
     }
     memset(m->params_host, 0, sizeof(StepParams));
     *m->status_host = 0;
+    const char *eager = getenv("PLAMO_HIP_EAGER_DECODE");
+    m->eager_decode = eager && *eager && strcmp(eager, "0") != 0;
     if (m->config.memory != PLAMO_METAL_STREAM)
         for (size_t i = 0; i < m->config.count && m->config.maps; ++i)
             if (!add_range(m, m->config.maps[i].base, m->config.maps[i].bytes)) {
@@ -1223,7 +1231,7 @@ int plamo_metal_forward(struct plamo_metal *m, struct model *model, uint64_t tok
     plan.row_cap = short_ctx ? kDecodeShortRows : 0;
     int dispatches = 0;
     begin_timing(m);
-    if (plan.special) {
+    if (plan.special || m->eager_decode) {
         if (!encode_decode(m, model, plan, &dispatches)) return fail(m);
     } else {
         hipGraphExec_t &g = short_ctx ? m->graph_short : m->graph;

@@ -281,3 +281,44 @@ def test_short_context_graph_boundary(pinned):
             cpu.close()
     finally:
         syn.close()
+
+
+def test_eager_decode_matches_graph(monkeypatch):
+    """PLAMO_HIP_EAGER_DECODE=1 (read when the backend opens) launches the
+    decode step's kernels one by one instead of replaying the captured graph:
+    the same kernels with the same arguments, so logits, states and the
+    appended KV rows are bit-identical to the graph's, in the short-context
+    graph's range and past it."""
+    cfg = dict(plamo_hip.CONFIGS["c4"], layers=2, vocab=1000)
+    syn = plamo_hip.Synthetic(**cfg, pattern=2, seed=808)
+    runs = []
+    try:
+        for eager in ("", "1"):
+            say(f"eager={eager!r}")
+            monkeypatch.setenv("PLAMO_HIP_EAGER_DECODE", eager)
+            gpu = syn.instance(pinned=True)
+            be = plamo_hip.Backend(syn)
+            monkeypatch.delenv("PLAMO_HIP_EAGER_DECODE")
+            try:
+                gpu.fill_kv(250, 5)
+                token, out = 3, []
+                for step in range(10):  # rows 251..260 cross the 256-row boundary
+                    assert be.forward(gpu, token) == 1
+                    out.append((gpu.logits().copy(), gpu.state().copy(), gpu.normalized().copy()))
+                    token = int(np.argmax(out[-1][0]))
+                kv = [gpu.kv(i, w).copy() for i in range(cfg["layers"])
+                      for w in ("k", "v", "rot")]
+                info = be.info()
+                assert info.errors == 0 and info.cpu_fallbacks == 0, info.note.decode()
+                runs.append((out, kv))
+            finally:
+                be.close()
+                gpu.close()
+    finally:
+        syn.close()
+    (graph_out, graph_kv), (eager_out, eager_kv) = runs
+    for a, b in zip(graph_out, eager_out):
+        for x, y in zip(a, b):
+            assert np.array_equal(x, y)
+    for x, y in zip(graph_kv, eager_kv):
+        assert np.array_equal(x, y)
