@@ -121,6 +121,39 @@ __device__ __forceinline__ bool arrive_last(uint32_t *counter, uint32_t expected
     return *flag;
 }
 
+// Counts the calling block in *counter after every store of the block has
+// completed; the result is not needed, so the add does not wait for its
+// return. Call from all threads.
+__device__ __forceinline__ void signal_done(uint32_t *counter) {
+    wait_stores();
+    __syncthreads();
+    if (threadIdx.x == 0)
+        (void)__hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Bounded wait until *counter reaches target, for a whole block: wave 0
+// polls (one request per poll) while the other waves wait at the barrier, so
+// a launch's waiting blocks keep the counter's memory channel free for the
+// arrivals. Returns false when the wait gave up after `limit` polls; call
+// from every thread of the block.
+__device__ __forceinline__ bool block_wait(const uint32_t *counter, uint32_t target,
+                                           uint32_t limit, int *flag) {
+    if (threadIdx.x < 64) {
+        bool ok = true;
+        for (uint32_t spins = 0;
+             __hip_atomic_load(counter, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target;) {
+            __builtin_amdgcn_s_sleep(2);
+            if (++spins >= limit) {
+                ok = false;
+                break;
+            }
+        }
+        if (threadIdx.x == 0) *flag = ok;
+    }
+    __syncthreads();
+    return *flag;
+}
+
 // The device's own status for the host: block 0 of a launch that carries a
 // Prologue with `status_out` copies the step's error word there (the decode
 // head, a pinned host word), so a step whose bounded wait gave up is reported
@@ -2441,7 +2474,7 @@ __device__ __forceinline__ void attention_block(const DecodeAttention &a, uint32
         }
     }
     if (splits == 1) {
-        if (done) arrive_last(done, 0xffffffffu, &is_last);
+        if (done) signal_done(done);
         return;
     }
     // The last block of this KV head merges the partials. They were written
@@ -2488,7 +2521,7 @@ __device__ __forceinline__ void attention_block(const DecodeAttention &a, uint32
         else
             a.out[(uint64_t)(kvh * G + g) * DIM + d] = o / sum;
     }
-    if (done) arrive_last(done, 0xffffffffu, &is_last);
+    if (done) signal_done(done);
 }
 
 template <int DIM, int G, int ROWS>
@@ -2519,9 +2552,10 @@ constexpr size_t kAttentionOLds = 96 * 1024;
 template <int KC>
 __device__ __forceinline__ void oproj_block(const AttentionO &f, uint32_t ob) {
     constexpr int U = kORows;
+    __shared__ int waited;
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const uint32_t r0 = (ob * kAttnWaves + wave) * U;
-    if (r0 >= f.rows) return;
+    if (ob * kAttnWaves * U >= f.rows) return;  // block-uniform: the wait below is block-wide
     u32x4 wv[U][KC];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
@@ -2533,17 +2567,8 @@ __device__ __forceinline__ void oproj_block(const AttentionO &f, uint32_t ob) {
     // Zero in the step's parameters means: wait for every KV head, up to
     // 2^22 polls. Other values exist for tests, which raise the target past
     // the heads so that the wait gives up while every block still exits.
-    const uint32_t target = f.heads + f.a.params->wait_extra;
     const uint32_t limit = f.a.params->wait_limit ? f.a.params->wait_limit : (1u << 22);
-    uint32_t spins = 0;
-    bool ok = true;
-    while (__hip_atomic_load(f.done, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
-        __builtin_amdgcn_s_sleep(2);
-        if (++spins >= limit) {
-            ok = false;
-            break;
-        }
-    }
+    const bool ok = block_wait(f.done, f.heads + f.a.params->wait_extra, limit, &waited);
     float acc[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) acc[u] = 0.0f;
@@ -2567,7 +2592,7 @@ __device__ __forceinline__ void oproj_block(const AttentionO &f, uint32_t ob) {
         const float v = wave_sum(acc[u]);
         if (lane == 0 && r0 + u < f.rows) f.y[r0 + u] = ok ? v : __builtin_nanf("");
     }
-    if (!ok && lane == 0) atomicOr(f.error, 1u);
+    if (!ok && threadIdx.x == 0) atomicOr(f.error, 1u);
 }
 
 template <int DIM, int G, int KC, int ROWS>
