@@ -491,7 +491,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(const uint16_t *__restri
                                                         uint64_t rows, uint64_t cols,
                                                         Prologue pro, float *__restrict__ y,
                                                         uint64_t half) {
-    extern __shared__ float xs[];
+    extern __shared__ __attribute__((aligned(16))) float xs[];
     __shared__ float red[4];
     const uint32_t bid = blockIdx.x, nblocks = gridDim.x;
     const uint32_t n = (uint32_t)cols;
@@ -668,7 +668,7 @@ __global__ __launch_bounds__(kThreads) void gemv_regp_kernel(const uint16_t *__r
     // WPR waves share a step, each holding KC of the row's KC * WPR chunks;
     // their sums meet in LDS.
     constexpr int GROUPS = 4 / WPR;
-    extern __shared__ float xs[];
+    extern __shared__ __attribute__((aligned(16))) float xs[];
     __shared__ float red[4];
     __shared__ float part[4][U];
     const uint32_t bid = blockIdx.x, nblocks = gridDim.x;
@@ -1337,7 +1337,7 @@ constexpr uint32_t kSkinnyLdsFloats = 12288;          // X slice budget per bloc
 template <int R, int U>
 __global__ __launch_bounds__(256) void skinny_gemm_kernel(SkinnyGemm g) {
     constexpr uint32_t KS = 32 * U;
-    extern __shared__ float xs[];  // [t][kc + 4]
+    extern __shared__ __attribute__((aligned(16))) float xs[];  // [t][kc + 4]
     __shared__ int is_last;
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const uint32_t col = lane & 15, q = lane >> 4;
@@ -1546,7 +1546,7 @@ template <int T>
 __global__ __launch_bounds__(256, 1) void token_gemv_kernel(TokenGemv g) {
     static_assert(T >= 1 && T <= (int)kTokenMax, "token count the plan admits");
     constexpr uint32_t U = kTokenU, KC = kTokenKC, UT = U * T, H = U / 2;
-    extern __shared__ float tg_lds[];
+    extern __shared__ __attribute__((aligned(16))) float tg_lds[];
     // X slice [T][ks], each 512-column chunk as two planes: lane l's columns
     // 8 l .. 8 l + 3 at 4 l, and 8 l + 4 .. 8 l + 7 at 256 + 4 l, so both of a
     // lane's 16-byte reads are 1 KB contiguous across the wave.
@@ -1648,26 +1648,20 @@ __global__ __launch_bounds__(256, 1) void token_gemv_kernel(TokenGemv g) {
     load(a1, lu, ls);
     advance(lu, ls);
     __builtin_amdgcn_sched_barrier(0);
-    // Stage X[:, slice] (eight loads in flight per thread and trip). Indices
-    // past the end repeat the last element, loads and stores alike, so every
-    // load is consumed by a store and none is left pending into the loop
-    // (where its register would be waited for on every trip).
-    const uint32_t q4 = g.ks / 4, total = T * q4;
-    for (uint32_t e0 = threadIdx.x; e0 < total; e0 += 256 * 8) {
-        f32x4 v[8];
-        uint32_t at[8];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            at[j] = min(e0 + 256 * j, total - 1);
-            const uint32_t tok = at[j] / q4, c = (at[j] - tok * q4) * 4;
-            v[j] = *(const f32x4 *)(g.x + (uint64_t)tok * g.ldx + k0 + c);
+    // Stage X[:, slice]: one direct-to-LDS load per (token, chunk, plane),
+    // spread over the waves and all in flight at once. Lane l's 16 bytes land
+    // at 16 l of the plane, which is the plane layout above: plane 0 of a
+    // chunk holds columns 8 l .. 8 l + 3, plane 1 columns 8 l + 4 .. 8 l + 7.
+    {
+        const uint32_t planes = T * chunks * 2;
+        for (uint32_t i = wave; i < planes; i += 4) {
+            const uint32_t t = i / (2 * chunks), r = i - t * 2 * chunks, c = r >> 1, pl = r & 1;
+            const float *src = g.x + (uint64_t)t * g.ldx + k0 + c * 512 + pl * 4 + lane * 8;
+            __builtin_amdgcn_global_load_lds(
+                src, (__attribute__((address_space(3))) void *)(xs + t * g.ks + c * 512 + pl * 256),
+                16, 0, 0);
         }
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            // Column c (a multiple of 4) of a chunk: lane c / 8, plane c / 4 % 2.
-            const uint32_t f = at[j] * 4, c = f % 512;
-            *(f32x4 *)(xs + (f - c) + (c / 4 % 2) * 256 + c / 8 * 4) = v[j];
-        }
+        __builtin_amdgcn_s_waitcnt(0);
     }
     __syncthreads();
     const uint32_t items = mine * nsub;
@@ -2150,7 +2144,7 @@ __device__ __forceinline__ void attention_block(const DecodeAttention &a, uint32
     constexpr int KR = RW / 4;               // key rows per lane
     constexpr uint32_t HALF = DIM / 2;
     constexpr uint32_t rec = DIM + 2;
-    extern __shared__ float smem[];
+    extern __shared__ __attribute__((aligned(16))) float smem[];
     __shared__ int is_last;
     __shared__ float stats[G][2];  // per head: maximum, sum of exp
     const uint32_t width = a.kh * DIM;
@@ -2720,7 +2714,7 @@ hipError_t launch_decode_attention(hipStream_t stream, const DecodeAttention &a)
 constexpr int kQT = 16, kKT = 32;
 __global__ __launch_bounds__(kThreads) void prompt_attention_kernel(PromptAttention a,
                                                                     uint32_t split_rows) {
-    extern __shared__ float smem[];
+    extern __shared__ __attribute__((aligned(16))) float smem[];
     const uint32_t dim = a.dim, half = dim / 2, width = a.kh * dim;
     float *qs = smem;                    // [kQT][dim]
     float *ks = qs + kQT * dim;          // [kKT][dim + 1]
@@ -2992,7 +2986,7 @@ __global__ __launch_bounds__(64 * G) void prompt_attention_mfma_kernel(PromptAtt
     constexpr int VS = DIM + 16;  // V row stride: the two 16-lane halves use opposite banks
     constexpr int PS = kMK + 2;   // P row stride
     constexpr int NT = DIM / 16;  // output column tiles of 16
-    extern __shared__ float smem[];
+    extern __shared__ __attribute__((aligned(16))) float smem[];
     float *ks = smem;          // [kMK][KS]
     float *vs = ks + kMK * KS; // [kMK][VS]
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
