@@ -144,6 +144,7 @@ struct plamo_metal {
     // Candidate results kept for commit.
     float *v_state = nullptr, *v_norm = nullptr, *v_logits = nullptr, *v_prop = nullptr;
     float *v_host = nullptr;  // pinned: states | normalized | logits | proposals
+    bool prop_on_host = true;  // the last verify copied its proposals into v_host
     uint32_t *v_next = nullptr, *v_next_host = nullptr;
     void *v_argmax = nullptr;  // argmax partials of the candidate logits
     CopyRow *copy_table = nullptr, *copy_table_host = nullptr;
@@ -350,14 +351,14 @@ bool alloc_verify(plamo_metal *m, uint64_t L, uint64_t h, uint64_t V) {
     m->v_prop = dev_alloc<float>(m, prop);
     m->v_next = dev_alloc<uint32_t>(m, kMaxVerify);
     m->v_argmax = dev_alloc<char>(m, argmax_scratch_bytes(kMaxVerify));
-    m->copy_table = dev_alloc<CopyRow>(m, 3 * kMaxLayers);
+    m->copy_table = dev_alloc<CopyRow>(m, 6 * kMaxLayers);  // device and host rows per layer
     bool ok = state && m->v_norm && m->v_logits && m->v_prop && m->v_next && m->v_argmax &&
               m->copy_table;
     ok = ok && hipHostMalloc((void **)&m->v_host, (kMaxVerify * (2 * h + V) + prop) * 4,
                              hipHostMallocDefault) == hipSuccess;
     ok = ok && hipHostMalloc((void **)&m->v_next_host, kMaxVerify * 4, hipHostMallocDefault) ==
                    hipSuccess;
-    ok = ok && hipHostMalloc((void **)&m->copy_table_host, 3 * kMaxLayers * sizeof(CopyRow),
+    ok = ok && hipHostMalloc((void **)&m->copy_table_host, 6 * kMaxLayers * sizeof(CopyRow),
                              hipHostMallocDefault) == hipSuccess;
     if (!ok) {
         (void)hipGetLastError();
@@ -1394,10 +1395,10 @@ int run_prompt(plamo_metal *m, struct model *model, const uint32_t *ids, uint64_
             ++n;
         }
         float *prop_k = nullptr, *prop_v = nullptr, *prop_r = nullptr;
-        if (verify) {
-            prop_k = m->v_prop + ((i * 3 + 0) * kMaxVerify) * m->max_width;
-            prop_v = m->v_prop + ((i * 3 + 1) * kMaxVerify) * m->max_width;
-            prop_r = m->v_prop + ((i * 3 + 2) * kMaxVerify) * m->max_width;
+        if (verify) {  // [layer][K, V, rotated K][T][width]
+            prop_k = m->v_prop + ((i * 3 + 0) * T) * m->max_width;
+            prop_v = m->v_prop + ((i * 3 + 1) * T) * m->max_width;
+            prop_r = m->v_prop + ((i * 3 + 2) * T) * m->max_width;
         }
         QkvPost qp{};
         qp.qkv = qkv;
@@ -1545,8 +1546,13 @@ int run_prompt(plamo_metal *m, struct model *model, const uint32_t *ids, uint64_
                                   hipMemcpyDeviceToHost, s));
         HIP_FAIL(m, hipMemcpyAsync(m->v_host + 2 * kMaxVerify * h, m->v_logits, T * V * 4,
                                   hipMemcpyDeviceToHost, s));
-        HIP_FAIL(m, hipMemcpyAsync(m->v_host + kMaxVerify * (2 * h + V), m->v_prop,
-                                  L * 3 * kMaxVerify * m->max_width * 4, hipMemcpyDeviceToHost, s));
+        // The candidates' cache rows reach the host at commit, for the
+        // committed candidate only: written in place by the commit's copy
+        // kernel when the host arrays are device-visible, else from this copy.
+        m->prop_on_host = !m->host_direct;
+        if (m->prop_on_host)
+            HIP_FAIL(m, hipMemcpyAsync(m->v_host + kMaxVerify * (2 * h + V), m->v_prop,
+                                      L * 3 * T * m->max_width * 4, hipMemcpyDeviceToHost, s));
         HIP_FAIL(m, hipMemcpyAsync(m->v_next_host, m->v_next, T * 4, hipMemcpyDeviceToHost, s));
         HIP_FAIL(m, hipMemcpyAsync(m->status_host, &m->params_dev->error, 4, hipMemcpyDeviceToHost, s));
         n += 3;
@@ -1637,19 +1643,26 @@ int plamo_metal_commit(struct plamo_metal *m, struct model *model, uint64_t inde
     // Candidate rows were rotated at positions prefix + index; ordinary
     // appends only copy them (runtime/metal_model.m:881-900). A full sliding
     // window is rebased on the device instead.
+    const uint64_t T = m->verification_tokens;
     const float *prop_host = m->v_host + kMaxVerify * (2 * h + V);
     uint32_t entries = 0;
     begin_timing(m);
     for (uint64_t i = 0; i < L; ++i) {
         Layer &d = m->layers[i];
         const struct cache *c = model->layers[i]->mixer->cache;
-        float *pk = m->v_prop + ((i * 3 + 0) * kMaxVerify + index) * m->max_width;
-        float *pv = m->v_prop + ((i * 3 + 1) * kMaxVerify + index) * m->max_width;
-        float *pr = m->v_prop + ((i * 3 + 2) * kMaxVerify + index) * m->max_width;
+        float *pk = m->v_prop + ((i * 3 + 0) * T + index) * m->max_width;
+        float *pv = m->v_prop + ((i * 3 + 1) * T + index) * m->max_width;
+        float *pr = m->v_prop + ((i * 3 + 2) * T + index) * m->max_width;
         if (c->count < c->capacity) {
             m->copy_table_host[entries++] = CopyRow{pk, d.k + c->count * d.width, d.width};
             m->copy_table_host[entries++] = CopyRow{pv, d.v + c->count * d.width, d.width};
             m->copy_table_host[entries++] = CopyRow{pr, d.rot + c->count * d.width, d.width};
+            if (!m->prop_on_host) {
+                const uint64_t o = c->count * d.width;
+                m->copy_table_host[entries++] = CopyRow{pk, d.host_k + o, d.width};
+                m->copy_table_host[entries++] = CopyRow{pv, d.host_v + o, d.width};
+                m->copy_table_host[entries++] = CopyRow{pr, d.host_rot + o, d.width};
+            }
         } else {
             HIP_FAIL(m, launch_window_store(m->stream, d.k, d.v, d.rot, pk, pv, d.width,
                                            m->ropes[d.rope].table, as<float>(m->p_window),
@@ -1669,19 +1682,30 @@ int plamo_metal_commit(struct plamo_metal *m, struct model *model, uint64_t inde
         struct mixer *mx = model->layers[i]->mixer;
         struct cache *c = mx->cache;
         struct rotation *r = mx->rotation;
-        const float *hk = prop_host + ((i * 3 + 0) * kMaxVerify + index) * m->max_width;
-        const float *hv = prop_host + ((i * 3 + 1) * kMaxVerify + index) * m->max_width;
-        const float *hr = prop_host + ((i * 3 + 2) * kMaxVerify + index) * m->max_width;
+        const float *hk = prop_host + ((i * 3 + 0) * T + index) * m->max_width;
+        const float *hv = prop_host + ((i * 3 + 1) * T + index) * m->max_width;
+        const float *hr = prop_host + ((i * 3 + 2) * T + index) * m->max_width;
         if (c->count < c->capacity) {
-            memcpy(c->k + c->count * c->width, hk, c->width * 4);
-            memcpy(c->v + c->count * c->width, hv, c->width * 4);
-            memcpy(r->out + c->count * c->width, hr, c->width * 4);
+            if (m->prop_on_host) {
+                memcpy(c->k + c->count * c->width, hk, c->width * 4);
+                memcpy(c->v + c->count * c->width, hv, c->width * 4);
+                memcpy(r->out + c->count * c->width, hr, c->width * 4);
+            }
             ++c->count;
         } else {
             memmove(c->k, c->k + c->width, (c->capacity - 1) * c->width * 4);
             memmove(c->v, c->v + c->width, (c->capacity - 1) * c->width * 4);
-            memcpy(c->k + (c->capacity - 1) * c->width, hk, c->width * 4);
-            memcpy(c->v + (c->capacity - 1) * c->width, hv, c->width * 4);
+            float *kk = c->k + (c->capacity - 1) * c->width, *vv = c->v + (c->capacity - 1) * c->width;
+            if (m->prop_on_host) {
+                memcpy(kk, hk, c->width * 4);
+                memcpy(vv, hv, c->width * 4);
+            } else if (hipMemcpy(kk, m->v_prop + ((i * 3 + 0) * T + index) * m->max_width,
+                                 c->width * 4, hipMemcpyDeviceToHost) != hipSuccess ||
+                       hipMemcpy(vv, m->v_prop + ((i * 3 + 1) * T + index) * m->max_width,
+                                 c->width * 4, hipMemcpyDeviceToHost) != hipSuccess) {
+                problem(m, "cannot mirror a committed row");
+                return fail(m);
+            }
             if (hipMemcpy(r->out, d.rot, c->capacity * c->width * 4, hipMemcpyDeviceToHost) !=
                 hipSuccess) {
                 problem(m, "cannot mirror rotated keys");

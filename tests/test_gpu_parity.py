@@ -112,10 +112,12 @@ def test_prefill_then_decode(h, inter, dim, capacity):
         s.close()
 
 
-def test_verify_and_commit():
-    # tests/metal_decode.c:309-365
+@pytest.mark.parametrize("pinned", [False, True])
+def test_verify_and_commit(pinned):
+    # tests/metal_decode.c:309-365. pinned: commit writes the accepted rows
+    # into the host arrays from the device (no proposal copy at verify).
     s = tiny(h=128, inter=257, dim=128, capacity=40)
-    a, b = s.instance(), s.instance()
+    a, b = s.instance(pinned=pinned), s.instance()
     be = plamo_hip.Backend(s)
     try:
         ids = [(i * 7 + 3) % 17 for i in range(16)]
@@ -174,10 +176,11 @@ def test_verify_and_commit():
         s.close()
 
 
-def test_verify_through_sliding_window():
+@pytest.mark.parametrize("pinned", [False, True])
+def test_verify_through_sliding_window(pinned):
     # Candidates past a full sliding window: commit rebases the window on the device.
     s = tiny(h=24, inter=40, dim=6, capacity=64)
-    a, b = s.instance(), s.instance()
+    a, b = s.instance(pinned=pinned), s.instance()
     be = plamo_hip.Backend(s)
     try:
         ids = [4, 9, 1, 16, 2]
