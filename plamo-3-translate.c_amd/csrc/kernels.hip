@@ -353,31 +353,36 @@ __device__ __forceinline__ void gemv_store(float *y, uint64_t rows, uint64_t pai
 
 // Norm prologue (src/forward.s layer entry: offset-1 RMSNorm, with the
 // previous branch's residual folded in). The one-round-trip form gives each
-// thread a contiguous 16-element slice: its loads go out in one batch, then
-// two block reductions. prologue_load issues the loads, prologue_finish
-// writes the normalized vector to LDS (and block 0 the optional state/norm
-// copies).
+// thread a contiguous slice of E elements (16 up to 4096 columns, 24 for
+// 6144): its loads go out in one batch, then two block reductions.
+// prologue_load issues the loads, prologue_finish writes the normalized vector
+// to LDS (and block 0 the optional state/norm copies).
+template <int E>
 struct ProloguePart {
-    float sv[16], bv[16], wv[16], rv[16];
+    float sv[E], bv[E], wv[E], rv[E];
     uint32_t i0;
     bool fast, mine;
 };
-__device__ __forceinline__ void prologue_begin(const Prologue &pro, uint32_t n, ProloguePart &pp) {
-    pp.fast = pro.w && n % 16 == 0 && n <= 16 * kThreads &&
+template <int E>
+__device__ __forceinline__ void prologue_begin(const Prologue &pro, uint32_t n,
+                                               ProloguePart<E> &pp) {
+    pp.fast = pro.w && n % E == 0 && n <= E * kThreads &&
               !(((uintptr_t)pro.src | (uintptr_t)pro.w |
                  (pro.branch ? ((uintptr_t)pro.branch | (uintptr_t)pro.rw) : 0)) & 15);
-    pp.i0 = threadIdx.x * 16;
+    pp.i0 = threadIdx.x * E;
     pp.mine = pp.fast && pp.i0 < n;
 }
-__device__ __forceinline__ void prologue_load(const Prologue &pro, ProloguePart &pp) {
+template <int E>
+__device__ __forceinline__ void prologue_load(const Prologue &pro, ProloguePart<E> &pp) {
+    static_assert(E % 8 == 0, "whole 16-byte loads");
     if (pp.mine) {
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
+        for (int q = 0; q < E / 4; ++q) {
             f32x4 a = *(const f32x4 *)(pro.src + pp.i0 + 4 * q);
             pp.sv[4 * q] = a.x; pp.sv[4 * q + 1] = a.y; pp.sv[4 * q + 2] = a.z; pp.sv[4 * q + 3] = a.w;
         }
 #pragma unroll
-        for (int q = 0; q < 2; ++q) {
+        for (int q = 0; q < E / 8; ++q) {
             u32x4 u = *(const u32x4 *)(pro.w + pp.i0 + 8 * q);
             uint32_t uu[4] = {u.x, u.y, u.z, u.w};
 #pragma unroll
@@ -388,12 +393,12 @@ __device__ __forceinline__ void prologue_load(const Prologue &pro, ProloguePart 
         }
         if (pro.branch) {
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
+            for (int q = 0; q < E / 4; ++q) {
                 f32x4 a = *(const f32x4 *)(pro.branch + pp.i0 + 4 * q);
                 pp.bv[4 * q] = a.x; pp.bv[4 * q + 1] = a.y; pp.bv[4 * q + 2] = a.z; pp.bv[4 * q + 3] = a.w;
             }
 #pragma unroll
-            for (int q = 0; q < 2; ++q) {
+            for (int q = 0; q < E / 8; ++q) {
                 u32x4 u = *(const u32x4 *)(pro.rw + pp.i0 + 8 * q);
                 uint32_t uu[4] = {u.x, u.y, u.z, u.w};
 #pragma unroll
@@ -405,42 +410,44 @@ __device__ __forceinline__ void prologue_load(const Prologue &pro, ProloguePart 
         }
     }
 }
-__device__ __forceinline__ void prologue_finish(const Prologue &pro, uint32_t n, ProloguePart &pp,
-                                                float *xs, float *red, uint32_t bid) {
+template <int E>
+__device__ __forceinline__ void prologue_finish(const Prologue &pro, uint32_t n,
+                                                ProloguePart<E> &pp, float *xs, float *red,
+                                                uint32_t bid) {
     if (pp.fast) {
         float ss = 0.0f;
         if (pro.branch) {
             if (pp.mine)
 #pragma unroll
-                for (int k = 0; k < 16; ++k) {
+                for (int k = 0; k < E; ++k) {
                     float t = pp.bv[k] * pp.bv[k];
                     ss = ss + t;
                 }
             const float ib = block_inverse_from_partial(ss, n, red);
             if (pp.mine)
 #pragma unroll
-                for (int k = 0; k < 16; ++k) {
+                for (int k = 0; k < E; ++k) {
                     float b = pp.bv[k] * ib;
                     float scale = pp.rv[k] + pro.roffset;
                     pp.sv[k] = pp.sv[k] + b * scale;
                 }
             if (bid == 0 && pro.state_out && pp.mine)
 #pragma unroll
-                for (int q = 0; q < 4; ++q)
+                for (int q = 0; q < E / 4; ++q)
                     *(f32x4 *)(pro.state_out + pp.i0 + 4 * q) =
                         f32x4{pp.sv[4 * q], pp.sv[4 * q + 1], pp.sv[4 * q + 2], pp.sv[4 * q + 3]};
             ss = 0.0f;
         }
         if (pp.mine)
 #pragma unroll
-            for (int k = 0; k < 16; ++k) {
+            for (int k = 0; k < E; ++k) {
                 float t = pp.sv[k] * pp.sv[k];
                 ss = ss + t;
             }
         const float is = block_inverse_from_partial(ss, n, red);
         if (pp.mine)
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
+            for (int q = 0; q < E / 4; ++q) {
                 f32x4 x;
                 x.x = (pp.sv[4 * q] * is) * (pp.wv[4 * q] + pro.offset);
                 x.y = (pp.sv[4 * q + 1] * is) * (pp.wv[4 * q + 1] + pro.offset);
@@ -502,7 +509,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(const uint16_t *__restri
     const uint64_t p0 = (uint64_t)bid * 4 + wave;
     // Batches of this wave: nb per row pair, pairs p0, p0 + step, ...
     const uint64_t total = p0 < pairs ? ((pairs - 1 - p0) / step + 1) * nb : 0;
-    ProloguePart pp;
+    ProloguePart<16> pp;
     prologue_begin(pro, n, pp);
     prologue_load(pro, pp);
     __builtin_amdgcn_sched_barrier(0);
@@ -682,7 +689,8 @@ __global__ __launch_bounds__(kThreads) void gemv_regp_kernel(const uint16_t *__r
     const uint32_t step = nblocks * GROUPS;
     const uint32_t ubase = bid * GROUPS;
     const uint32_t u0 = ubase + grp;
-    ProloguePart pp;
+    // cols = 512 * KC * WPR: 16 elements per thread up to 4096, 24 for 6144.
+    ProloguePart<(KC * WPR * 512 > 16 * kThreads ? 24 : 16)> pp;
     prologue_begin(pro, n, pp);
     prologue_load(pro, pp);
     __builtin_amdgcn_sched_barrier(0);
