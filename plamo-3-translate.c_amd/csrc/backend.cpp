@@ -132,7 +132,7 @@ struct plamo_metal {
     // arguments). For profilers that trace kernel launches but not graph
     // replays.
     bool eager_decode = false;
-    float *host_state = nullptr, *host_norm = nullptr;
+    float *host_state = nullptr, *host_norm = nullptr, *host_logits = nullptr;
     // The device's error word of the last call, copied by the call's last
     // kernel (or a copy) into pinned host memory; status_dev is its device view.
     uint32_t *status_host = nullptr, *status_dev = nullptr;
@@ -461,7 +461,8 @@ float *device_view(void *p) {
 void find_host_views(plamo_metal *m, struct model *model) {
     m->host_state = device_view(model->state);
     m->host_norm = device_view(model->normalized);
-    bool ok = m->host_state && m->host_norm && device_view(model->logits);
+    m->host_logits = device_view(model->logits);
+    bool ok = m->host_state && m->host_norm && m->host_logits;
     for (uint64_t i = 0; i < model->count; ++i) {
         Layer &d = m->layers[i];
         struct mixer *mx = model->layers[i]->mixer;
@@ -944,11 +945,12 @@ int encode_decode(plamo_metal *m, struct model *model, const DecodePlan &plan, i
     ph.norm_out = plan.direct ? m->host_norm : norm_out;
     ph.status = &m->params_dev->error;
     ph.status_out = m->status_dev;
-    HIP_TRY(m, launch_gemv(s, m->head, V, h, ph, logits, 0, blocks));
+    // Direct: the head's rows go straight to the host logits as they are
+    // computed (the PCIe writes overlap the head's weight stream; a copy
+    // after the head would add its transfer to the step).
+    HIP_TRY(m, launch_gemv(s, m->head, V, h, ph, plan.direct ? m->host_logits : logits, 0, blocks));
     ++n;
-    if (plan.direct)
-        HIP_TRY(m, hipMemcpyAsync(model->logits, logits, V * 4, hipMemcpyDeviceToHost, s));
-    else
+    if (!plan.direct)
         HIP_TRY(m, hipMemcpyAsync(m->outbox_host, m->outbox, m->outbox_floats * 4,
                                   hipMemcpyDeviceToHost, s));
     *dispatches = n;
