@@ -3032,19 +3032,37 @@ __global__ __launch_bounds__(64 * G) void prompt_attention_mfma_kernel(PromptAtt
     for (uint32_t k0 = lo_min; k0 < hi_max; k0 += kMK) {
         const uint32_t nk = hi_max - k0 < (uint32_t)kMK ? hi_max - k0 : kMK;
         __syncthreads();  // the previous tile's K, V and P reads are done
-        for (uint32_t i = threadIdx.x; i < kMK * (DIM / 4); i += 64 * G) {
-            const uint32_t r = i / (DIM / 4), c = (i % (DIM / 4)) * 4;
-            const uint32_t vrow = k0 + (r < nk ? r : nk - 1);
-            const float *kp = vrow < a.prefix ? a.k_cache + (uint64_t)vrow * width
-                                              : a.k_new + (uint64_t)(vrow - a.prefix) * width;
-            const float *vp = vrow < a.prefix ? a.v_cache + (uint64_t)vrow * width
-                                              : a.v_new + (uint64_t)(vrow - a.prefix) * width;
-            f32x4 kv = *(const f32x4 *)(kp + (uint64_t)kvh * DIM + c);
-            f32x4 vv = *(const f32x4 *)(vp + (uint64_t)kvh * DIM + c);
-            if (r >= nk) kv = vv = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-            float *kd = ks + r * KS + c;
-            kd[0] = kv.x; kd[1] = kv.y; kd[2] = kv.z; kd[3] = kv.w;
-            *(f32x4 *)(vs + r * VS + c) = vv;
+        // The tile's K and V rows, up to four 16-byte pieces of each per
+        // thread in flight before any is stored (one round trip per round).
+        constexpr uint32_t kPieces = kMK * (DIM / 4), kStride = 64 * G;
+        constexpr uint32_t kPer = (kPieces + kStride - 1) / kStride, kRound = kPer < 4 ? kPer : 4;
+        for (uint32_t base = 0; base < kPer; base += kRound) {
+            f32x4 kv[kRound], vv[kRound];
+#pragma unroll
+            for (uint32_t j = 0; j < kRound; ++j) {
+                const uint32_t i = threadIdx.x + (base + j) * kStride;
+                const uint32_t r = i / (DIM / 4), c = (i % (DIM / 4)) * 4;
+                const uint32_t vrow = k0 + (r < nk ? r : nk - 1);
+                const float *kp = vrow < a.prefix ? a.k_cache + (uint64_t)vrow * width
+                                                  : a.k_new + (uint64_t)(vrow - a.prefix) * width;
+                const float *vp = vrow < a.prefix ? a.v_cache + (uint64_t)vrow * width
+                                                  : a.v_new + (uint64_t)(vrow - a.prefix) * width;
+                if (i < kPieces) {
+                    kv[j] = *(const f32x4 *)(kp + (uint64_t)kvh * DIM + c);
+                    vv[j] = *(const f32x4 *)(vp + (uint64_t)kvh * DIM + c);
+                }
+            }
+#pragma unroll
+            for (uint32_t j = 0; j < kRound; ++j) {
+                const uint32_t i = threadIdx.x + (base + j) * kStride;
+                if (i >= kPieces) continue;
+                const uint32_t r = i / (DIM / 4), c = (i % (DIM / 4)) * 4;
+                f32x4 k = kv[j], v = vv[j];
+                if (r >= nk) k = v = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+                float *kd = ks + r * KS + c;
+                kd[0] = k.x; kd[1] = k.y; kd[2] = k.z; kd[3] = k.w;
+                *(f32x4 *)(vs + r * VS + c) = v;
+            }
         }
         __syncthreads();
         // S for keys k0 + col and k0 + 16 + col.
