@@ -1026,7 +1026,7 @@ static hipError_t gemm_variant(hipStream_t stream, const float *x, uint64_t x_st
 // The GEMM block is 4 waves as 2 x 2, each wave WM x WN tiles of 32 x 32, so
 // a block covers BM = 64 WM token rows by BN = 64 WN weight rows; K advances
 // 32 per stage through double-buffered LDS (two blocks per CU for WN = 2), with
-// three stages in flight in registers. Each block starts its K loop at its
+// PD stages in flight in registers. Each block starts its K loop at its
 // own stage (rotating): weight rows are a multiple of 4 KB apart, so blocks in
 // lockstep would all read one memory channel. LDS rows are 64 bytes with their four
 // 16-byte granules XOR-swizzled by row, which keeps the fragment reads and the
@@ -1078,7 +1078,7 @@ __global__ __launch_bounds__(256) void split_planes_kernel(const float *x, uint6
                                              pack_hi16(lo[4], lo[5]), pack_hi16(lo[6], lo[7])};
 }
 
-template <int WM, int WN, int GM = 2, int GN = 2>
+template <int WM, int WN, int GM = 2, int GN = 2, int PD = 3>
 __global__ __launch_bounds__(64 * GM * GN, (WN > 2 || GM * GN > 4) ? 1 : 2) void gemm_split_kernel(
     GemmSplit g) {
     constexpr int NT = 64 * GM * GN;                             // threads: GM x GN waves
@@ -1127,7 +1127,7 @@ __global__ __launch_bounds__(64 * GM * GN, (WN > 2 || GM * GN > 4) ? 1 : 2) void
         wsrc[i] = g.w + (uint64_t)min(n0 + r, g.n - 1) * g.k + 8 * q;
         wdst[i] = AG + r * 4 + swizzle(r, q);
     }
-    u32x4 av[3][APT], wv[3][WPT];
+    u32x4 av[PD][APT], wv[PD][WPT];
     auto load = [&](int slot, uint32_t stage) {
         uint32_t s = first + min(stage, nst - 1);
         s = s < nst ? s : s - nst;
@@ -1186,28 +1186,26 @@ __global__ __launch_bounds__(64 * GM * GN, (WN > 2 || GM * GN > 4) ? 1 : 2) void
         }
     };
 
-    // Stage j lives in register slot j % 3 and LDS buffer j % 2. Loads are
+    // Stage j lives in register slot j % PD and LDS buffer j % 2. Loads are
     // unconditional (clamped to the last stage) so the compiler keeps exact
-    // wait counts; the step count is padded to a multiple of three.
-    load(0, 0);
-    load(1, 1);
-    load(2, 2);
+    // wait counts; the step count is padded to a multiple of PD.
+#pragma unroll
+    for (int sl = 0; sl < PD; ++sl) load(sl, sl);
     store(0, 0);
     __syncthreads();
     int buf = 0;
     auto step = [&](uint32_t j, int slot) {
-        load(slot, j + 3);
+        load(slot, j + PD);
         if (j < nst) {
             compute(buf);
-            if (j + 1 < nst) store((slot + 1) % 3, buf ^ 1);
+            if (j + 1 < nst) store((slot + 1) % PD, buf ^ 1);
         }
         __syncthreads();
         buf ^= 1;
     };
-    for (uint32_t j = 0; j < nst; j += 3) {
-        step(j, 0);
-        step(j + 1, 1);
-        step(j + 2, 2);
+    for (uint32_t j = 0; j < nst; j += PD) {
+#pragma unroll
+        for (int sl = 0; sl < PD; ++sl) step(j + sl, sl);
     }
 
     // D layout of v_mfma_f32_32x32x16: value v of lane l is row
@@ -1268,7 +1266,7 @@ __global__ __launch_bounds__(64 * GM * GN, (WN > 2 || GM * GN > 4) ? 1 : 2) void
         }
 }
 
-template <int WM, int WN, int GM = 2, int GN = 2>
+template <int WM, int WN, int GM = 2, int GN = 2, int PD = 3>
 static hipError_t gemm_split_variant(hipStream_t stream, GemmSplit g, const GemmWorkspace &ws) {
     constexpr uint32_t BM = 32 * WM * GM, BN = 32 * WN * GN;
     const uint32_t nt = (g.n + BN - 1) / BN, mt = (g.t + BM - 1) / BM;
@@ -1298,12 +1296,12 @@ static hipError_t gemm_split_variant(hipStream_t stream, GemmSplit g, const Gemm
     const size_t lds = 2 * (size_t)(3 * BM * 4 + BN * 4) * sizeof(u32x4);
     static bool attr = false;
     if (!attr) {
-        hipError_t e = hipFuncSetAttribute((const void *)gemm_split_kernel<WM, WN, GM, GN>,
+        hipError_t e = hipFuncSetAttribute((const void *)gemm_split_kernel<WM, WN, GM, GN, PD>,
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (e != hipSuccess) return e;
         attr = true;
     }
-    gemm_split_kernel<WM, WN, GM, GN><<<dim3(nt, mt, splits), 64 * GM * GN, lds, stream>>>(g);
+    gemm_split_kernel<WM, WN, GM, GN, PD><<<dim3(nt, mt, splits), 64 * GM * GN, lds, stream>>>(g);
     return hipGetLastError();
 }
 
@@ -1877,8 +1875,10 @@ hipError_t launch_gemm(hipStream_t stream, const float *x, uint64_t x_stride, co
         if (tokens <= 64)
             return wide ? gemm_split_variant<1, 4>(stream, g, *ws)
                         : gemm_split_variant<1, 2>(stream, g, *ws);
-        return wide ? gemm_split_variant<2, 2, 2, 4>(stream, g, *ws)
-                    : gemm_split_variant<2, 2>(stream, g, *ws);
+        // Four K stages in registers ahead of the LDS stage (3: TTFT@128
+        // 11.43 ms, 4: 11.19, 5 and 6 slower).
+        return wide ? gemm_split_variant<2, 2, 2, 4, 4>(stream, g, *ws)
+                    : gemm_split_variant<2, 2, 2, 2, 4>(stream, g, *ws);
     }
     if (tokens <= 16) return gemm_variant<16, 64>(stream, x, x_stride, w, rows, cols, tokens, y, y_stride);
     return gemm_variant<64, 64>(stream, x, x_stride, w, rows, cols, tokens, y, y_stride);
