@@ -556,7 +556,7 @@ def main() -> int:
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path "
-              f"(--gpus {args.gpus} is not supported; shard design is in DESIGN.md)",
+              f"(--gpus {args.gpus} is not supported)",
               file=sys.stderr)
         return 2
     if args.speculative:
