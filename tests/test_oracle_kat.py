@@ -564,3 +564,47 @@ def test_argmax_and_hashes(oracle, hip):
     assert oracle.oracle_fnv1a(None, 0, basis) == basis
     assert oracle.oracle_fnv1a(ctypes.c_char_p(b"a"), 1, basis) == 0xAF63DC4C8601EC8C
     assert oracle.oracle_fnv1a(ctypes.c_char_p(b"foobar"), 6, basis) == 0x85944171F73967E8
+
+
+ARGMAX_CHECK = r"""
+import sys
+import numpy as np
+sys.path[:0] = sys.argv[1:3]
+import oracle_lib, plamo_hip
+from ctypes import POINTER, c_float
+hip, oracle = plamo_hip.load(), oracle_lib.load()
+P = lambda a: a.ctypes.data_as(POINTER(c_float))
+rng = np.random.default_rng(11)
+cases = [np.array([-0.0, 0.0, -1.0], np.float32), np.array([float("-inf")] * 97, np.float32)]
+for n in list(range(1, 140)) + [1000, 100000]:
+    x = rng.integers(-3, 4, size=n).astype(np.float32)
+    cases.append(x)
+    y = rng.standard_normal(n).astype(np.float32)
+    cases.append(y)
+    if n > 2:
+        z = y.copy()
+        z[rng.integers(0, n)] = np.nan
+        cases.append(z)
+        w = x.copy()
+        w[-1] = w.max() + 1
+        cases.append(w)
+for x in cases:
+    assert hip.plamo_argmax(P(x), x.size) == oracle.oracle_argmax(P(x), x.size), (x.size, x[:8])
+print("ok", len(cases))
+"""
+
+
+@pytest.mark.parametrize("isa", ["sse2", "avx2", "avx512"])
+def test_argmax_every_vector_width(oracle, hip, isa):
+    # plamo_argmax picks its vector width once per process (PLAMO_ARGMAX_ISA
+    # caps it): each width against the oracle's sequential scan, in a process
+    # of its own. Where the CPU lacks a width the next narrower one runs.
+    import subprocess
+    import sys
+    here = Path(__file__).resolve().parent
+    env = dict(__import__("os").environ, PLAMO_ARGMAX_ISA=isa)
+    r = subprocess.run([sys.executable, "-c", ARGMAX_CHECK, str(here),
+                        str(here.parent / "plamo-3-translate.c_amd")],
+                       capture_output=True, text=True, env=env, timeout=300)
+    assert r.returncode == 0, r.stdout + r.stderr
+    assert r.stdout.startswith("ok")
