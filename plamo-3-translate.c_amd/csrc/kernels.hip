@@ -1767,30 +1767,52 @@ static bool token_plan(uint64_t rows, uint64_t cols, uint64_t tokens, uint64_t h
         rows >= (1u << 30) || (half && (half % (kTokenU / 2) || rows != 2 * half)))
         return false;
     const uint64_t chunks = cols / 512;
-    uint64_t slices = 0;
-    for (uint64_t d = 1; d <= chunks && !slices; ++d)
-        if (chunks % d == 0 && tokens * (cols / d) * 4 <= kTokenXBytes) slices = d;
-    if (!slices) return false;
-    const uint64_t ks = cols / slices;
     const uint64_t units = half ? half / (kTokenU / 2) : (rows + kTokenU - 1) / kTokenU;
-    uint64_t blocks = std::max<uint64_t>(1, 1ull * std::max<uint32_t>(cus, 1) / slices);
-    blocks = std::min<uint64_t>(blocks, (units + 3) / 4);
     const uint64_t budget = kTokenLdsBytes / 4 / tokens;  // floats per block per token
-    if (budget <= ks) return false;
-    const uint64_t max_local = (budget - ks) / (4 * kTokenU);
-    if (!max_local) return false;
-    uint64_t local = (units + 4 * blocks - 1) / (4 * blocks);
-    if (local > max_local) {
-        blocks = (units + 4 * max_local - 1) / (4 * max_local);
-        local = (units + 4 * blocks - 1) / (4 * blocks);
+    // The grid for `slices` K slices; false when its X slice or staged sums
+    // do not fit.
+    auto shape = [&](uint64_t slices, TokenPlan &q) {
+        const uint64_t ks = cols / slices;
+        if (tokens * ks * 4 > kTokenXBytes || budget <= ks) return false;
+        uint64_t blocks = std::max<uint64_t>(1, 1ull * std::max<uint32_t>(cus, 1) / slices);
+        blocks = std::min<uint64_t>(blocks, (units + 3) / 4);
+        const uint64_t max_local = (budget - ks) / (4 * kTokenU);
+        if (!max_local) return false;
+        uint64_t local = (units + 4 * blocks - 1) / (4 * blocks);
+        if (local > max_local) {
+            blocks = (units + 4 * max_local - 1) / (4 * max_local);
+            local = (units + 4 * blocks - 1) / (4 * blocks);
+        }
+        if (blocks > 65535) return false;
+        q.slices = (uint32_t)slices;
+        q.ks = (uint32_t)ks;
+        q.blocks = (uint32_t)blocks;
+        q.local = (uint32_t)local;
+        q.lds = (size_t)tokens * (ks + 4 * kTokenU * local) * 4;
+        return true;
+    };
+    // The fewest slices that fit. When those leave the waves unequal shares
+    // of the units, the slicing with the shortest longest-wave stream (units
+    // x slice columns) instead, if it is at least a tenth shorter: with 4
+    // tokens, a 24576-column down projection in 3 slices leaves its 768 units
+    // 3 or 2 per wave (68.8 us), in 4 slices exactly 3.
+    bool found = false;
+    uint64_t best = 0, first_cost = 0;
+    for (uint64_t d = 1; d <= chunks; ++d) {
+        TokenPlan q;
+        if (chunks % d || !shape(d, q)) continue;
+        const uint64_t cost = (uint64_t)q.local * q.ks;
+        if (!found) {
+            p = q;
+            best = first_cost = cost;
+            found = true;
+            if (units % (4ull * q.blocks) == 0) break;  // equal shares
+        } else if (cost < best && cost * 10 <= first_cost * 9) {
+            p = q;
+            best = cost;
+        }
     }
-    if (blocks > 65535) return false;
-    p.slices = (uint32_t)slices;
-    p.ks = (uint32_t)ks;
-    p.blocks = (uint32_t)blocks;
-    p.local = (uint32_t)local;
-    p.lds = (size_t)tokens * (ks + 4 * kTokenU * local) * 4;
-    return true;
+    return found;
 }
 
 // The token GEMV stages up to kTokenLdsBytes, above the default 64 KiB.
