@@ -15,6 +15,7 @@ namespace plamo {
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kThreads = 256;
 
@@ -2041,12 +2042,86 @@ __global__ __launch_bounds__(kThreads) void residual_norm_rows_kernel(
     }
 }
 
+// residual_norm_rows_kernel with 16-byte accesses (width a multiple of 4):
+// thread i holds elements 4 (i + kThreads j) .. + 3.
+template <int NV>
+__global__ __launch_bounds__(kThreads) void residual_norm_rows4_kernel(
+    float *state, const float *branch, const uint16_t *wr, float off_r, const uint16_t *wn,
+    float off_n, float *norm, uint64_t norm_stride, uint32_t width) {
+    __shared__ float red[4];
+    const uint64_t row = blockIdx.x;
+    const uint32_t groups = width / 4;
+    f32x4 b[NV], st[NV];
+    u32x2 gr[NV], gn[NV];
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        const uint32_t g = threadIdx.x + kThreads * j;
+        const uint32_t c = (g < groups ? g : groups - 1) * 4;
+        const bool in = g < groups;
+        const f32x4 bv = *(const f32x4 *)(branch + row * width + c);
+        const f32x4 sv = *(const f32x4 *)(state + row * width + c);
+        const u32x2 rv = *(const u32x2 *)(wr + c), nv = *(const u32x2 *)(wn + c);
+        const f32x4 z = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        b[j] = in ? bv : z;
+        st[j] = in ? sv : z;
+        gr[j] = in ? rv : u32x2{0u, 0u};
+        gn[j] = in ? nv : u32x2{0u, 0u};
+    }
+    float ss = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NV; ++j)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const float t = b[j][e] * b[j][e];
+            ss = ss + t;
+        }
+    const float inv = block_inverse_from_partial(ss, width, red);
+    float ss2 = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        const uint32_t g = threadIdx.x + kThreads * j;
+        const uint32_t w[4] = {gr[j].x & 0xffffu, gr[j].x >> 16, gr[j].y & 0xffffu, gr[j].y >> 16};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const float v = (b[j][e] * inv) * (bf16f(w[e]) + off_r);
+            st[j][e] = st[j][e] + v;
+            const float t = st[j][e] * st[j][e];
+            ss2 = ss2 + t;
+        }
+        if (g < groups) *(f32x4 *)(state + row * width + 4 * g) = st[j];
+    }
+    const float inv2 = block_inverse_from_partial(ss2, width, red);
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        const uint32_t g = threadIdx.x + kThreads * j;
+        const uint32_t w[4] = {gn[j].x & 0xffffu, gn[j].x >> 16, gn[j].y & 0xffffu, gn[j].y >> 16};
+        f32x4 o;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o[e] = (st[j][e] * inv2) * (bf16f(w[e]) + off_n);
+        if (g < groups) *(f32x4 *)(norm + row * norm_stride + 4 * g) = o;
+    }
+}
+
 hipError_t launch_residual_norm_rows(hipStream_t stream, float *state, const float *branch,
                                      const uint16_t *wr, float off_r, const uint16_t *wn,
                                      float off_n, float *norm, uint64_t norm_stride,
                                      uint64_t width, uint64_t rows) {
     if (!rows) return hipSuccess;
     const uint32_t w = (uint32_t)width;
+    if (width % 4 == 0 && norm_stride % 4 == 0 && !((uintptr_t)state & 15) &&
+        !((uintptr_t)branch & 15) && !((uintptr_t)norm & 15) && !((uintptr_t)wr & 7) &&
+        !((uintptr_t)wn & 7) && width <= 8192) {
+        if (width <= 2048)
+            residual_norm_rows4_kernel<2><<<(unsigned)rows, kThreads, 0, stream>>>(
+                state, branch, wr, off_r, wn, off_n, norm, norm_stride, w);
+        else if (width <= 4096)
+            residual_norm_rows4_kernel<4><<<(unsigned)rows, kThreads, 0, stream>>>(
+                state, branch, wr, off_r, wn, off_n, norm, norm_stride, w);
+        else
+            residual_norm_rows4_kernel<8><<<(unsigned)rows, kThreads, 0, stream>>>(
+                state, branch, wr, off_r, wn, off_n, norm, norm_stride, w);
+        return hipGetLastError();
+    }
     if (width <= 2048)
         residual_norm_rows_kernel<8><<<(unsigned)rows, kThreads, 0, stream>>>(
             state, branch, wr, off_r, wn, off_n, norm, norm_stride, w);
