@@ -1377,6 +1377,12 @@ int run_prompt(plamo_metal *m, struct model *model, const uint32_t *ids, uint64_
     // `normed` says the next layer's input norm is already in `norm`.
     const bool fuse_rows = h <= 8192;
     bool normed = false, final_normed = false;
+    // Prompts past 16 tokens take the matrix-core GEMM, which reads X as
+    // three BF16 planes: the norms that feed QKV and gate/up write them as
+    // they write their rows, so those projections skip their own split.
+    // qkv_planes: the planes of the next QKV input are already written.
+    uint16_t *const planes = ws->planes;
+    bool qkv_planes = false;
     for (uint64_t i = 0; i < L; ++i) {
         Layer &d = m->layers[i];
         const struct cache *c = model->layers[i]->mixer->cache;
@@ -1385,11 +1391,15 @@ int run_prompt(plamo_metal *m, struct model *model, const uint32_t *ids, uint64_
         const RopeTable &rope = m->ropes[d.rope];
         const uint64_t qkv_w = (uint64_t)(d.qh + 2 * d.kh) * d.dim, aw = (uint64_t)d.qh * d.dim;
         if (!normed) {
-            HIP_FAIL(m, launch_norm_rows(s, state, h, pre, 1.0f, norm, h, h, T));
+            const uint32_t tp = gemm_planes_rows(T, h, ws);
+            HIP_FAIL(m, launch_norm_rows(s, state, h, pre, 1.0f, norm, h, h, T, tp ? planes : nullptr,
+                                         tp));
+            qkv_planes = tp != 0;
             ++n;
         }
         normed = false;
-        HIP_FAIL(m, launch_gemm(s, norm, h, d.qkv, qkv_w, h, T, qkv, qkv_w, ws));
+        HIP_FAIL(m, launch_gemm(s, norm, h, d.qkv, qkv_w, h, T, qkv, qkv_w, ws, qkv_planes));
+        qkv_planes = false;
         ++n;
         if (stale[i] && (verify || !overflow[i])) {
             HIP_FAIL(m, launch_rerotate(s, d.k, d.rot, rope.table, c->count, d.kh, d.dim));
@@ -1515,21 +1525,28 @@ int run_prompt(plamo_metal *m, struct model *model, const uint32_t *ids, uint64_
             n += 5;
         } else {
             HIP_FAIL(m, launch_gemm(s, attn + first * aw, aw, d.o, h, aw, rows, branch, h, ws));
+            bool gu_planes = false;
             if (fuse_rows) {
+                const uint32_t tp = gemm_planes_rows(rows, h, ws);
                 HIP_FAIL(m, launch_residual_norm_rows(s, st, branch, post, kAttentionOffset, mpre,
-                                                     1.0f, norm, h, h, rows));
+                                                     1.0f, norm, h, h, rows, tp ? planes : nullptr,
+                                                     tp));
+                gu_planes = tp != 0;
             } else {
                 HIP_FAIL(m, launch_residual_rows(s, st, branch, post, kAttentionOffset, h, rows));
                 HIP_FAIL(m, launch_norm_rows(s, st, h, mpre, 1.0f, norm, h, h, rows));
                 ++n;
             }
-            HIP_FAIL(m, launch_gemm_swiglu(s, norm, h, d.gu, d.inter, h, rows, act, gu, ws));
+            HIP_FAIL(m, launch_gemm_swiglu(s, norm, h, d.gu, d.inter, h, rows, act, gu, ws,
+                                          gu_planes));
             HIP_FAIL(m, launch_gemm(s, act, d.inter, d.down, h, d.inter, rows, branch, h, ws));
             if (fuse_rows && i + 1 < L) {
+                const uint32_t tp = gemm_planes_rows(rows, h, ws);
                 HIP_FAIL(m, launch_residual_norm_rows(s, st, branch, mpost, kMlpOffset,
                                                      m->layers[i + 1].norms, 1.0f, norm, h, h,
-                                                     rows));
+                                                     rows, tp ? planes : nullptr, tp));
                 normed = true;
+                qkv_planes = tp != 0;
             } else if (fuse_rows && verify) {
                 HIP_FAIL(m, launch_residual_norm_rows(s, st, branch, mpost, kMlpOffset,
                                                      m->final_norm, 1.0f, m->v_norm, h, h, rows));

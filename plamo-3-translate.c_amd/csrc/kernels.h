@@ -89,19 +89,31 @@ uint64_t gemm_plane_elems(uint64_t tokens, uint64_t cols);
 // the decode GEMV. Otherwise, with a workspace, more than one token and K a
 // multiple of 64: BF16 matrix cores on the exact three-term split of X; else
 // FP32 MFMA with BF16 weights widened in LDS.
+// planes_ready: the BF16 planes of X for the matrix-core path are already in
+// ws->planes (written by launch_norm_rows / launch_residual_norm_rows with
+// gemm_planes_rows(tokens, cols, ws) rows); other paths read x as usual.
 hipError_t launch_gemm(hipStream_t, const float *x, uint64_t x_stride, const uint16_t *w,
                        uint64_t rows, uint64_t cols, uint64_t tokens, float *y,
-                       uint64_t y_stride, const GemmWorkspace *ws);
+                       uint64_t y_stride, const GemmWorkspace *ws, bool planes_ready = false);
+// The padded rows of the BF16 planes launch_gemm's matrix-core path reads for
+// `tokens` rows of `cols` columns, or 0 when another path takes the call.
+uint32_t gemm_planes_rows(uint64_t tokens, uint64_t cols, const GemmWorkspace *ws);
 // Multi-row RMSNorm; with branch: state += rms(branch) * (bf16(w) + offset).
+// With planes, the normalized rows also go into the BF16 planes of
+// launch_gemm's matrix-core path, `padded` rows (gemm_planes_rows of the
+// consuming projection; rows past `rows` zero), so that projection can take
+// planes_ready.
 hipError_t launch_norm_rows(hipStream_t, const float *x, uint64_t x_stride, const uint16_t *w,
                             float offset, float *y, uint64_t y_stride, uint64_t width,
-                            uint64_t rows);
+                            uint64_t rows, uint16_t *planes = nullptr, uint32_t padded = 0);
 // launch_residual_rows followed by launch_norm_rows of the updated rows into
-// norm, in one launch (width <= 8192; hipErrorInvalidValue otherwise).
+// norm, in one launch (width <= 8192; hipErrorInvalidValue otherwise), planes
+// as launch_norm_rows (16-byte-aligned rows only; hipErrorInvalidValue else).
 hipError_t launch_residual_norm_rows(hipStream_t, float *state, const float *branch,
                                      const uint16_t *wr, float off_r, const uint16_t *wn,
                                      float off_n, float *norm, uint64_t norm_stride,
-                                     uint64_t width, uint64_t rows);
+                                     uint64_t width, uint64_t rows, uint16_t *planes = nullptr,
+                                     uint32_t padded = 0);
 hipError_t launch_residual_rows(hipStream_t, float *state, const float *branch,
                                 const uint16_t *w, float offset, uint64_t width, uint64_t rows);
 hipError_t launch_swiglu_rows(hipStream_t, const float *gate_up, float *out,
@@ -112,7 +124,7 @@ hipError_t launch_swiglu_rows(hipStream_t, const float *gate_up, float *out,
 // launch_swiglu_rows.
 hipError_t launch_gemm_swiglu(hipStream_t, const float *x, uint64_t x_stride, const uint16_t *w,
                               uint64_t intermediate, uint64_t cols, uint64_t tokens, float *act,
-                              float *gate_up, const GemmWorkspace *ws);
+                              float *gate_up, const GemmWorkspace *ws, bool planes_ready = false);
 
 // Q/K head RMSNorm + RoPE + cache append for `tokens` rows of one layer.
 struct QkvPost {

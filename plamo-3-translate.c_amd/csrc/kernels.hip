@@ -1268,7 +1268,8 @@ __global__ __launch_bounds__(64 * GM * GN, (WN > 2 || GM * GN > 4) ? 1 : 2) void
 }
 
 template <int WM, int WN, int GM = 2, int GN = 2, int PD = 3>
-static hipError_t gemm_split_variant(hipStream_t stream, GemmSplit g, const GemmWorkspace &ws) {
+static hipError_t gemm_split_variant(hipStream_t stream, GemmSplit g, const GemmWorkspace &ws,
+                                     bool planes_ready = false) {
     constexpr uint32_t BM = 32 * WM * GM, BN = 32 * WN * GN;
     const uint32_t nt = (g.n + BN - 1) / BN, mt = (g.t + BM - 1) / BM;
     const uint32_t tiles = nt * mt, stages = g.k / kSplitBK;
@@ -1292,8 +1293,9 @@ static hipError_t gemm_split_variant(hipStream_t stream, GemmSplit g, const Gemm
     // Grouping needs whole turns of the 8 XCDs: (weight tiles x splits) % 8 == 0.
     g.xcd_group = mt > 1 && (nt * splits) % 8 == 0;
     const uint64_t elems = (uint64_t)g.tp * g.k;
-    split_planes_kernel<<<(unsigned)((elems / 8 + 255) / 256), 256, 0, stream>>>(
-        g.x, g.ldx, g.t, g.tp, g.k, ws.planes);
+    if (!planes_ready)
+        split_planes_kernel<<<(unsigned)((elems / 8 + 255) / 256), 256, 0, stream>>>(
+            g.x, g.ldx, g.t, g.tp, g.k, ws.planes);
     const size_t lds = 2 * (size_t)(3 * BM * 4 + BN * 4) * sizeof(u32x4);
     static bool attr = false;
     if (!attr) {
@@ -1888,9 +1890,19 @@ uint64_t gemm_plane_elems(uint64_t tokens, uint64_t cols) {
     return 3 * ((tokens + 127) / 128 * 128) * cols;
 }
 
+uint32_t gemm_planes_rows(uint64_t tokens, uint64_t cols, const GemmWorkspace *ws) {
+    if (tokens <= kSkinnyTokens || tokens >= (1u << 31) || cols % (2 * kSplitBK) ||
+        cols > (1u << 30) || !ws || !ws->planes)
+        return 0;
+    const uint64_t bm = tokens <= 64 ? 64 : 128, tp = (tokens + bm - 1) / bm * bm;
+    return 3 * tp * cols <= ws->plane_elems && gemm_plane_elems(tokens, cols) <= ws->plane_elems
+               ? (uint32_t)tp
+               : 0;
+}
+
 hipError_t launch_gemm(hipStream_t stream, const float *x, uint64_t x_stride, const uint16_t *w,
                        uint64_t rows, uint64_t cols, uint64_t tokens, float *y,
-                       uint64_t y_stride, const GemmWorkspace *ws) {
+                       uint64_t y_stride, const GemmWorkspace *ws, bool planes_ready) {
     if (!tokens || !rows) return hipSuccess;
     {
         hipError_t e = launch_token_gemv(stream, x, x_stride, w, rows, cols, tokens, 0, y,
@@ -1928,12 +1940,12 @@ hipError_t launch_gemm(hipStream_t stream, const float *x, uint64_t x_stride, co
         // per MFMA and half the re-reads of X.
         const bool wide = (rows + 255) / 256 * ((tokens + 127) / 128) >= 64;
         if (tokens <= 64)
-            return wide ? gemm_split_variant<1, 4>(stream, g, *ws)
-                        : gemm_split_variant<1, 2>(stream, g, *ws);
+            return wide ? gemm_split_variant<1, 4>(stream, g, *ws, planes_ready)
+                        : gemm_split_variant<1, 2>(stream, g, *ws, planes_ready);
         // Four K stages in registers ahead of the LDS stage (3: TTFT@128
         // 11.43 ms, 4: 11.19, 5 and 6 slower).
-        return wide ? gemm_split_variant<2, 2, 2, 4, 4>(stream, g, *ws)
-                    : gemm_split_variant<2, 2, 2, 2, 4>(stream, g, *ws);
+        return wide ? gemm_split_variant<2, 2, 2, 4, 4>(stream, g, *ws, planes_ready)
+                    : gemm_split_variant<2, 2, 2, 2, 4>(stream, g, *ws, planes_ready);
     }
     if (tokens <= 16) return gemm_variant<16, 64>(stream, x, x_stride, w, rows, cols, tokens, y, y_stride);
     return gemm_variant<64, 64>(stream, x, x_stride, w, rows, cols, tokens, y, y_stride);
@@ -1942,13 +1954,13 @@ hipError_t launch_gemm(hipStream_t stream, const float *x, uint64_t x_stride, co
 hipError_t launch_gemm_swiglu(hipStream_t stream, const float *x, uint64_t x_stride,
                               const uint16_t *w, uint64_t intermediate, uint64_t cols,
                               uint64_t tokens, float *act, float *gate_up,
-                              const GemmWorkspace *ws) {
+                              const GemmWorkspace *ws, bool planes_ready) {
     if (!tokens || !intermediate) return hipSuccess;
     hipError_t e = launch_token_gemv(stream, x, x_stride, w, 2 * intermediate, cols, tokens,
                                      intermediate, act, intermediate, ws);
     if (e != hipErrorNotSupported) return e;
     e = launch_gemm(stream, x, x_stride, w, 2 * intermediate, cols, tokens, gate_up,
-                    2 * intermediate, ws);
+                    2 * intermediate, ws, planes_ready);
     if (e != hipSuccess) return e;
     return launch_swiglu_rows(stream, gate_up, act, intermediate, tokens);
 }
@@ -1968,18 +1980,45 @@ __global__ __launch_bounds__(kThreads) void norm_rows_kernel(const float *x, uin
     }
 }
 
+// Columns c .. c + 3 of row `row` into the BF16 planes of launch_gemm's
+// matrix-core path (the layout split_planes_kernel writes: [c / 32][plane]
+// [padded row][c % 32], the exact three-term split).
+__device__ __forceinline__ void write_planes4(uint16_t *planes, uint32_t padded, uint32_t row,
+                                              uint32_t c, f32x4 v) {
+    uint32_t h[4], md[4], lo[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        h[e] = __float_as_uint(v[e]) & 0xffff0000u;
+        const float r = v[e] - __uint_as_float(h[e]);
+        md[e] = __float_as_uint(r) & 0xffff0000u;
+        lo[e] = __float_as_uint(r - __uint_as_float(md[e]));
+    }
+    const uint64_t at = ((uint64_t)(c / kSplitBK) * 3 * padded + row) * kSplitBK + c % kSplitBK;
+    const uint64_t pl = (uint64_t)padded * kSplitBK;
+    *(u32x2 *)(planes + at) = u32x2{pack_hi16(h[0], h[1]), pack_hi16(h[2], h[3])};
+    *(u32x2 *)(planes + at + pl) = u32x2{pack_hi16(md[0], md[1]), pack_hi16(md[2], md[3])};
+    *(u32x2 *)(planes + at + 2 * pl) = u32x2{pack_hi16(lo[0], lo[1]), pack_hi16(lo[2], lo[3])};
+}
+
 // norm_rows_kernel with the row held in registers, 16-byte accesses (width a
 // multiple of 4, at most 8192): every load goes out before the sum, where the
 // strided loop above waits on each in turn (C5 verify's first norm 15 us).
+// With planes, blocks past `rows` (up to `padded`) write zero planes only.
 template <int NV>
 __global__ __launch_bounds__(kThreads) void norm_rows4_kernel(const float *x, uint64_t x_stride,
                                                               const uint16_t *w, float offset,
                                                               float *y, uint64_t y_stride,
-                                                              uint32_t width) {
+                                                              uint32_t width, uint16_t *planes,
+                                                              uint32_t padded, uint32_t rows) {
     __shared__ float red[4];
+    const uint32_t groups = width / 4;
+    if (blockIdx.x >= rows) {
+        for (uint32_t i = threadIdx.x; i < groups; i += kThreads)
+            write_planes4(planes, padded, blockIdx.x, 4 * i, f32x4{0.0f, 0.0f, 0.0f, 0.0f});
+        return;
+    }
     const float *xr = x + blockIdx.x * x_stride;
     float *yr = y + blockIdx.x * y_stride;
-    const uint32_t groups = width / 4;
     f32x4 v[NV];
     u32x2 g[NV];
 #pragma unroll
@@ -2007,30 +2046,40 @@ __global__ __launch_bounds__(kThreads) void norm_rows4_kernel(const float *x, ui
         f32x4 o;
 #pragma unroll
         for (int e = 0; e < 4; ++e) o[e] = (v[j][e] * inv) * (bf16f(wb[e]) + offset);
-        if (i < groups) *(f32x4 *)(yr + 4 * i) = o;
+        if (i < groups) {
+            *(f32x4 *)(yr + 4 * i) = o;
+            if (planes) write_planes4(planes, padded, blockIdx.x, 4 * i, o);
+        }
     }
 }
 
 hipError_t launch_norm_rows(hipStream_t stream, const float *x, uint64_t x_stride,
                             const uint16_t *w, float offset, float *y, uint64_t y_stride,
-                            uint64_t width, uint64_t rows) {
+                            uint64_t width, uint64_t rows, uint16_t *planes, uint32_t padded) {
     if (!rows) return hipSuccess;
+    if (planes && (padded < rows || width % (2 * kSplitBK))) return hipErrorInvalidValue;
     if (width % 4 == 0 && width <= 8192 && x_stride % 4 == 0 && y_stride % 4 == 0 &&
         !((uintptr_t)x & 15) && !((uintptr_t)y & 15) && !((uintptr_t)w & 7)) {
-        const uint32_t wd = (uint32_t)width;
+        const uint32_t wd = (uint32_t)width, n = (uint32_t)rows;
+        const unsigned grid = planes ? padded : n;
         if (width <= 2048)
-            norm_rows4_kernel<2><<<(unsigned)rows, kThreads, 0, stream>>>(x, x_stride, w, offset, y,
-                                                                          y_stride, wd);
+            norm_rows4_kernel<2><<<grid, kThreads, 0, stream>>>(x, x_stride, w, offset, y,
+                                                                y_stride, wd, planes, padded, n);
         else if (width <= 4096)
-            norm_rows4_kernel<4><<<(unsigned)rows, kThreads, 0, stream>>>(x, x_stride, w, offset, y,
-                                                                          y_stride, wd);
+            norm_rows4_kernel<4><<<grid, kThreads, 0, stream>>>(x, x_stride, w, offset, y,
+                                                                y_stride, wd, planes, padded, n);
         else
-            norm_rows4_kernel<8><<<(unsigned)rows, kThreads, 0, stream>>>(x, x_stride, w, offset, y,
-                                                                          y_stride, wd);
+            norm_rows4_kernel<8><<<grid, kThreads, 0, stream>>>(x, x_stride, w, offset, y,
+                                                                y_stride, wd, planes, padded, n);
         return hipGetLastError();
     }
     norm_rows_kernel<<<(unsigned)rows, kThreads, 0, stream>>>(x, x_stride, w, offset, y, y_stride,
                                                               (uint32_t)width);
+    if (planes) {
+        const uint64_t elems = (uint64_t)padded * width;
+        split_planes_kernel<<<(unsigned)((elems / 8 + 255) / 256), 256, 0, stream>>>(
+            y, y_stride, (uint32_t)rows, padded, (uint32_t)width, planes);
+    }
     return hipGetLastError();
 }
 
@@ -2104,10 +2153,16 @@ __global__ __launch_bounds__(kThreads) void residual_norm_rows_kernel(
 template <int NV>
 __global__ __launch_bounds__(kThreads) void residual_norm_rows4_kernel(
     float *state, const float *branch, const uint16_t *wr, float off_r, const uint16_t *wn,
-    float off_n, float *norm, uint64_t norm_stride, uint32_t width) {
+    float off_n, float *norm, uint64_t norm_stride, uint32_t width, uint16_t *planes,
+    uint32_t padded, uint32_t rows) {
     __shared__ float red[4];
     const uint64_t row = blockIdx.x;
     const uint32_t groups = width / 4;
+    if (blockIdx.x >= rows) {  // padding rows of the planes
+        for (uint32_t i = threadIdx.x; i < groups; i += kThreads)
+            write_planes4(planes, padded, blockIdx.x, 4 * i, f32x4{0.0f, 0.0f, 0.0f, 0.0f});
+        return;
+    }
     f32x4 b[NV], st[NV];
     u32x2 gr[NV], gn[NV];
 #pragma unroll
@@ -2155,30 +2210,38 @@ __global__ __launch_bounds__(kThreads) void residual_norm_rows4_kernel(
         f32x4 o;
 #pragma unroll
         for (int e = 0; e < 4; ++e) o[e] = (st[j][e] * inv2) * (bf16f(w[e]) + off_n);
-        if (g < groups) *(f32x4 *)(norm + row * norm_stride + 4 * g) = o;
+        if (g < groups) {
+            *(f32x4 *)(norm + row * norm_stride + 4 * g) = o;
+            if (planes) write_planes4(planes, padded, blockIdx.x, 4 * g, o);
+        }
     }
 }
 
 hipError_t launch_residual_norm_rows(hipStream_t stream, float *state, const float *branch,
                                      const uint16_t *wr, float off_r, const uint16_t *wn,
                                      float off_n, float *norm, uint64_t norm_stride,
-                                     uint64_t width, uint64_t rows) {
+                                     uint64_t width, uint64_t rows, uint16_t *planes,
+                                     uint32_t padded) {
     if (!rows) return hipSuccess;
+    if (planes && (padded < rows || width % (2 * kSplitBK))) return hipErrorInvalidValue;
     const uint32_t w = (uint32_t)width;
     if (width % 4 == 0 && norm_stride % 4 == 0 && !((uintptr_t)state & 15) &&
         !((uintptr_t)branch & 15) && !((uintptr_t)norm & 15) && !((uintptr_t)wr & 7) &&
         !((uintptr_t)wn & 7) && width <= 8192) {
+        const uint32_t n = (uint32_t)rows;
+        const unsigned grid = planes ? padded : n;
         if (width <= 2048)
-            residual_norm_rows4_kernel<2><<<(unsigned)rows, kThreads, 0, stream>>>(
-                state, branch, wr, off_r, wn, off_n, norm, norm_stride, w);
+            residual_norm_rows4_kernel<2><<<grid, kThreads, 0, stream>>>(
+                state, branch, wr, off_r, wn, off_n, norm, norm_stride, w, planes, padded, n);
         else if (width <= 4096)
-            residual_norm_rows4_kernel<4><<<(unsigned)rows, kThreads, 0, stream>>>(
-                state, branch, wr, off_r, wn, off_n, norm, norm_stride, w);
+            residual_norm_rows4_kernel<4><<<grid, kThreads, 0, stream>>>(
+                state, branch, wr, off_r, wn, off_n, norm, norm_stride, w, planes, padded, n);
         else
-            residual_norm_rows4_kernel<8><<<(unsigned)rows, kThreads, 0, stream>>>(
-                state, branch, wr, off_r, wn, off_n, norm, norm_stride, w);
+            residual_norm_rows4_kernel<8><<<grid, kThreads, 0, stream>>>(
+                state, branch, wr, off_r, wn, off_n, norm, norm_stride, w, planes, padded, n);
         return hipGetLastError();
     }
+    if (planes) return hipErrorInvalidValue;
     if (width <= 2048)
         residual_norm_rows_kernel<8><<<(unsigned)rows, kThreads, 0, stream>>>(
             state, branch, wr, off_r, wn, off_n, norm, norm_stride, w);
