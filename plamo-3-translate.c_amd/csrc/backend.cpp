@@ -1537,9 +1537,13 @@ int run_prompt(plamo_metal *m, struct model *model, const uint32_t *ids, uint64_
                 HIP_FAIL(m, launch_norm_rows(s, st, h, mpre, 1.0f, norm, h, h, rows));
                 ++n;
             }
+            // The activation goes to down's GEMM as BF16 planes only, when
+            // that GEMM takes the matrix-core route.
+            const uint32_t act_planes = gemm_planes_rows(rows, d.inter, ws);
             HIP_FAIL(m, launch_gemm_swiglu(s, norm, h, d.gu, d.inter, h, rows, act, gu, ws,
-                                          gu_planes));
-            HIP_FAIL(m, launch_gemm(s, act, d.inter, d.down, h, d.inter, rows, branch, h, ws));
+                                          gu_planes, act_planes));
+            HIP_FAIL(m, launch_gemm(s, act, d.inter, d.down, h, d.inter, rows, branch, h, ws,
+                                    act_planes != 0));
             if (fuse_rows && i + 1 < L) {
                 const uint32_t tp = gemm_planes_rows(rows, h, ws);
                 HIP_FAIL(m, launch_residual_norm_rows(s, st, branch, mpost, kMlpOffset,

@@ -116,15 +116,22 @@ hipError_t launch_residual_norm_rows(hipStream_t, float *state, const float *bra
                                      uint32_t padded = 0);
 hipError_t launch_residual_rows(hipStream_t, float *state, const float *branch,
                                 const uint16_t *w, float offset, uint64_t width, uint64_t rows);
+// With planes, writes the activation as the BF16 planes of a following
+// launch_gemm over `padded` rows (gemm_planes_rows of the activation) instead
+// of `out`.
 hipError_t launch_swiglu_rows(hipStream_t, const float *gate_up, float *out,
-                              uint64_t intermediate, uint64_t rows);
+                              uint64_t intermediate, uint64_t rows, uint16_t *planes = nullptr,
+                              uint32_t padded = 0);
 // act[t, i] = silu(g) * u of the gate/up projection (rows i and
 // intermediate + i of w): the token GEMV writes act directly; other shapes
 // go through launch_gemm into gate_up ([tokens][2 * intermediate]) and
-// launch_swiglu_rows.
+// launch_swiglu_rows. act_planes (gemm_planes_rows(tokens, intermediate, ws),
+// nonzero) writes the activation only as the workspace planes, for a
+// launch_gemm of act with planes_ready; shapes without that route fail.
 hipError_t launch_gemm_swiglu(hipStream_t, const float *x, uint64_t x_stride, const uint16_t *w,
                               uint64_t intermediate, uint64_t cols, uint64_t tokens, float *act,
-                              float *gate_up, const GemmWorkspace *ws, bool planes_ready = false);
+                              float *gate_up, const GemmWorkspace *ws, bool planes_ready = false,
+                              uint32_t act_planes = 0);
 
 // Q/K head RMSNorm + RoPE + cache append for `tokens` rows of one layer.
 struct QkvPost {

@@ -1904,6 +1904,9 @@ hipError_t launch_gemm(hipStream_t stream, const float *x, uint64_t x_stride, co
                        uint64_t rows, uint64_t cols, uint64_t tokens, float *y,
                        uint64_t y_stride, const GemmWorkspace *ws, bool planes_ready) {
     if (!tokens || !rows) return hipSuccess;
+    // planes_ready callers may not have written x: only the matrix-core route
+    // below may take them.
+    if (planes_ready && tokens <= kSkinnyTokens) return hipErrorInvalidValue;
     {
         hipError_t e = launch_token_gemv(stream, x, x_stride, w, rows, cols, tokens, 0, y,
                                          y_stride, ws);
@@ -1947,6 +1950,7 @@ hipError_t launch_gemm(hipStream_t stream, const float *x, uint64_t x_stride, co
         return wide ? gemm_split_variant<2, 2, 2, 4, 4>(stream, g, *ws, planes_ready)
                     : gemm_split_variant<2, 2, 2, 2, 4>(stream, g, *ws, planes_ready);
     }
+    if (planes_ready) return hipErrorInvalidValue;
     if (tokens <= 16) return gemm_variant<16, 64>(stream, x, x_stride, w, rows, cols, tokens, y, y_stride);
     return gemm_variant<64, 64>(stream, x, x_stride, w, rows, cols, tokens, y, y_stride);
 }
@@ -1954,15 +1958,18 @@ hipError_t launch_gemm(hipStream_t stream, const float *x, uint64_t x_stride, co
 hipError_t launch_gemm_swiglu(hipStream_t stream, const float *x, uint64_t x_stride,
                               const uint16_t *w, uint64_t intermediate, uint64_t cols,
                               uint64_t tokens, float *act, float *gate_up,
-                              const GemmWorkspace *ws, bool planes_ready) {
+                              const GemmWorkspace *ws, bool planes_ready, uint32_t act_planes) {
     if (!tokens || !intermediate) return hipSuccess;
     hipError_t e = launch_token_gemv(stream, x, x_stride, w, 2 * intermediate, cols, tokens,
                                      intermediate, act, intermediate, ws);
-    if (e != hipErrorNotSupported) return e;
+    if (e != hipErrorNotSupported) return act_planes && e == hipSuccess ? hipErrorInvalidValue : e;
     e = launch_gemm(stream, x, x_stride, w, 2 * intermediate, cols, tokens, gate_up,
                     2 * intermediate, ws, planes_ready);
     if (e != hipSuccess) return e;
-    return launch_swiglu_rows(stream, gate_up, act, intermediate, tokens);
+    if (act_planes && (!ws || !ws->planes || 3ull * act_planes * intermediate > ws->plane_elems))
+        return hipErrorInvalidValue;
+    return launch_swiglu_rows(stream, gate_up, act, intermediate, tokens,
+                              act_planes ? ws->planes : nullptr, act_planes);
 }
 
 // ---------------------------------------------------------------- row norms
@@ -2276,8 +2283,45 @@ __global__ __launch_bounds__(kThreads) void swiglu_rows_kernel(const float *gate
     out[e] = (g / d) * u;
 }
 
+// swiglu_rows_kernel straight into the BF16 planes of the down projection's
+// matrix-core GEMM (the layout and three-term split of split_planes_kernel),
+// four columns per thread; rows past `rows` (up to `padded`) get zero planes.
+// The FP32 activation is not written: the GEMM reads the planes only.
+__global__ __launch_bounds__(kThreads) void swiglu_planes_kernel(const float *gate_up,
+                                                                 uint32_t intermediate,
+                                                                 uint32_t rows, uint32_t padded,
+                                                                 uint16_t *planes) {
+    const uint32_t quads = intermediate / 4;
+    const uint64_t e = (uint64_t)blockIdx.x * kThreads + threadIdx.x;
+    if (e >= (uint64_t)quads * padded) return;
+    const uint32_t t = (uint32_t)(e / quads), c = (uint32_t)(e % quads) * 4;
+    f32x4 v = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    if (t < rows) {
+        const float *row = gate_up + (uint64_t)t * 2 * intermediate;
+        const f32x4 g = *(const f32x4 *)(row + c), u = *(const f32x4 *)(row + intermediate + c);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float d = plamo_exp(-g[i]) + 1.0f;
+            v[i] = (g[i] / d) * u[i];
+        }
+    }
+    write_planes4(planes, padded, t, c, v);
+}
+
 hipError_t launch_swiglu_rows(hipStream_t stream, const float *gate_up, float *out,
-                              uint64_t intermediate, uint64_t rows) {
+                              uint64_t intermediate, uint64_t rows, uint16_t *planes,
+                              uint32_t padded) {
+    if (planes) {
+        if (intermediate % (2 * kSplitBK) || intermediate >= (1u << 30) || padded < rows ||
+            ((uintptr_t)gate_up & 15))
+            return hipErrorInvalidValue;
+        const uint64_t threads = intermediate / 4 * padded;
+        if (!threads) return hipSuccess;
+        swiglu_planes_kernel<<<(unsigned)((threads + kThreads - 1) / kThreads), kThreads, 0,
+                               stream>>>(gate_up, (uint32_t)intermediate, (uint32_t)rows, padded,
+                                         planes);
+        return hipGetLastError();
+    }
     uint64_t total = intermediate * rows;
     if (!total) return hipSuccess;
     swiglu_rows_kernel<<<(unsigned)((total + kThreads - 1) / kThreads), kThreads, 0, stream>>>(
