@@ -122,9 +122,11 @@ int plamo_hip_rewind(struct plamo_metal *m, struct model *model, uint64_t steps)
 /* The backend keeps the device KV authoritative during a request and finds
  * host edits between calls (prompt-prefix restore, request reset, a draft
  * restore, a CPU step) from the per-layer count, processed_count, scale_bits
- * and the first and last 16 values of the last K and V rows. A caller that
- * rewrites rows while all of these stay unchanged calls this first: every
- * layer's host rows are then uploaded by the next call. No reference
+ * and the first and last 16 values of the last K and V rows. A prefill that
+ * starts on 1..64 cached rows (a restorable prompt prefix,
+ * runtime/prompt_cache.h:8) uploads them whatever these show. A caller that
+ * rewrites other rows while all of these stay unchanged calls this first:
+ * every layer's host rows are then uploaded by the next call. No reference
  * counterpart (the reference shares the host arrays with its GPU,
  * runtime/metal_model.m:57-119). */
 void plamo_hip_invalidate(struct plamo_metal *m);

@@ -159,6 +159,8 @@ struct plamo_metal {
     // with the attention's view of the allocation capped there.
     hipGraphExec_t graph_short = nullptr;
     uint64_t graph_short_epoch = 0;
+    // Kernels and copies each captured graph holds (counted at capture).
+    int graph_dispatches = 0, graph_short_dispatches = 0;
     std::vector<void *> allocations;
 };
 
@@ -687,10 +689,24 @@ bool resolve_layers(plamo_metal *m, struct model *model) {
 }
 
 // ---------------------------------------------------------------- host <-> device KV
+// Longest fixed prompt prefix the engine snapshots and restores
+// (PLAMO_PROMPT_PREFIX_LIMIT, runtime/prompt_cache.h:8).
+constexpr uint64_t kPromptPrefixLimit = 64;
+
 // Detects host-side KV edits since this backend's last return (prompt-prefix
 // restore, draft restore, request reset, a CPU step) and uploads the host rows.
 // Sets stale[i] when the device rotated rows must be rebuilt.
-int sync_from_host(plamo_metal *m, struct model *model, std::vector<char> &stale) {
+//
+// A prompt-prefix restore can leave every counter and the last rows as they
+// were: the engine prepares both translation prefixes in turn
+// (runtime/engine.c:357-381) and a request then restores the other one
+// (runtime/prompt_cache.c:62-82). The two template prefixes differ only in a
+// middle id (the target language) and end in the same id, and a layer-0 row
+// depends only on its token, so the sampled last rows agree too. So at prompt
+// entry (`prompt_entry`) a layer whose host count is a prefix length
+// (1..PLAMO_PROMPT_PREFIX_LIMIT) is always uploaded in full.
+int sync_from_host(plamo_metal *m, struct model *model, std::vector<char> &stale,
+                   bool prompt_entry) {
     stale.assign(model->count, 0);
     for (uint64_t i = 0; i < model->count; ++i) {
         Layer &d = m->layers[i];
@@ -699,7 +715,9 @@ int sync_from_host(plamo_metal *m, struct model *model, std::vector<char> &stale
         const struct rotation *r = mx->rotation;
         uint32_t scale = float_bits(model->scales[i]);
         const uint64_t last = c->count ? (c->count - 1) * c->width : 0, pf = probe_floats(c->width);
-        bool same = d.synced && d.count == c->count && d.processed == r->processed_count &&
+        const bool restorable = prompt_entry && c->count && c->count <= kPromptPrefixLimit;
+        bool same = !restorable && d.synced && d.count == c->count &&
+                    d.processed == r->processed_count &&
                     d.scale_bits == r->scale_bits &&
                     (!c->count || (probe_equal(c->k + last, c->width, d.last_kv.data()) &&
                                    probe_equal(c->v + last, c->width, d.last_kv.data() + pf)));
@@ -917,6 +935,7 @@ int encode_decode(plamo_metal *m, struct model *model, const DecodePlan &plan, i
             Prologue po{};
             po.src = m->attn;
             HIP_TRY(m, launch_gemv(s, d.o, h, (uint64_t)d.qh * d.dim, po, m->branch, 0, blocks));
+            ++n;
         }
         Prologue pg{};
         pg.src = cur;
@@ -931,7 +950,7 @@ int encode_decode(plamo_metal *m, struct model *model, const DecodePlan &plan, i
         Prologue pd{};
         pd.src = m->act;
         HIP_TRY(m, launch_gemv(s, d.down, h, d.inter, pd, m->down_out, 0, blocks));
-        n += 3;
+        n += 2;
         (void)mpost;
     }
     Prologue ph{};
@@ -1212,7 +1231,7 @@ int plamo_metal_forward(struct plamo_metal *m, struct model *model, uint64_t tok
     }
     if (!resolve_layers(m, model)) return 0;
     DecodePlan plan;
-    if (!sync_from_host(m, model, plan.stale)) return -1;
+    if (!sync_from_host(m, model, plan.stale, false)) return -1;
     plan.shift.assign(L, 0);
     for (uint64_t i = 0; i < L; ++i) {
         Layer &d = m->layers[i];
@@ -1239,6 +1258,7 @@ int plamo_metal_forward(struct plamo_metal *m, struct model *model, uint64_t tok
     } else {
         hipGraphExec_t &g = short_ctx ? m->graph_short : m->graph;
         uint64_t &g_epoch = short_ctx ? m->graph_short_epoch : m->graph_epoch;
+        int &g_dispatches = short_ctx ? m->graph_short_dispatches : m->graph_dispatches;
         if (!g || g_epoch != m->epoch) {
             if (g) (void)hipGraphExecDestroy(g);
             g = nullptr;
@@ -1255,8 +1275,9 @@ int plamo_metal_forward(struct plamo_metal *m, struct model *model, uint64_t tok
                 return fail(m);
             }
             g_epoch = m->epoch;
+            g_dispatches = dispatches;
         }
-        dispatches = (int)(2 + 5 * L);
+        dispatches = g_dispatches;
         if (hipGraphLaunch(g, m->stream) != hipSuccess) {
             (void)hipGetLastError();
             problem(m, "decode graph launch failed");
@@ -1333,7 +1354,7 @@ int run_prompt(plamo_metal *m, struct model *model, const uint32_t *ids, uint64_
     }
     if (!resolve_layers(m, model)) return 0;
     std::vector<char> stale;
-    if (!sync_from_host(m, model, stale)) return -1;
+    if (!sync_from_host(m, model, stale, !verify)) return -1;
     if (!ensure_prompt(m, model, T) || !ensure_window_scratch(m, model)) return -1;
     const GemmWorkspace *ws =
         gemm_workspace(m, T, std::max({h, m->max_attention, m->max_inter}));

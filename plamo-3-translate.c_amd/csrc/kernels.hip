@@ -1960,14 +1960,19 @@ hipError_t launch_gemm_swiglu(hipStream_t stream, const float *x, uint64_t x_str
                               uint64_t tokens, float *act, float *gate_up,
                               const GemmWorkspace *ws, bool planes_ready, uint32_t act_planes) {
     if (!tokens || !intermediate) return hipSuccess;
-    hipError_t e = launch_token_gemv(stream, x, x_stride, w, 2 * intermediate, cols, tokens,
-                                     intermediate, act, intermediate, ws);
-    if (e != hipErrorNotSupported) return act_planes && e == hipSuccess ? hipErrorInvalidValue : e;
-    e = launch_gemm(stream, x, x_stride, w, 2 * intermediate, cols, tokens, gate_up,
-                    2 * intermediate, ws, planes_ready);
-    if (e != hipSuccess) return e;
+    // Checked before anything is launched: a failure leaves the stream as it was.
     if (act_planes && (!ws || !ws->planes || 3ull * act_planes * intermediate > ws->plane_elems))
         return hipErrorInvalidValue;
+    // The token GEMV reads x and writes act as FP32 only: it takes neither
+    // input planes in place of x nor planes for the output.
+    if (!planes_ready && !act_planes) {
+        hipError_t e = launch_token_gemv(stream, x, x_stride, w, 2 * intermediate, cols, tokens,
+                                         intermediate, act, intermediate, ws);
+        if (e != hipErrorNotSupported) return e;
+    }
+    hipError_t e = launch_gemm(stream, x, x_stride, w, 2 * intermediate, cols, tokens, gate_up,
+                               2 * intermediate, ws, planes_ready);
+    if (e != hipSuccess) return e;
     return launch_swiglu_rows(stream, gate_up, act, intermediate, tokens,
                               act_planes ? ws->planes : nullptr, act_planes);
 }

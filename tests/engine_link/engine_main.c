@@ -8,7 +8,9 @@
  *       opens the model of $PLAMO_MODEL_DIR with the GPU backend and resident
  *       weights, prepares it (fixed prefixes captured), translates, and prints
  *       one JSON line: prompt ids, generated ids, cached prompt tokens, finish
- *       reason, decode steps and the backend's counters.
+ *       reason, decode steps and the backend's counters. With
+ *       $ENGINE_HOST_DUMP set, it also writes the model's final logits and
+ *       state there (raw float32, logits first).
  * Exit status 0 on success; 1 with the engine's error on stderr.
  */
 #include "engine.h"
@@ -92,6 +94,16 @@ int main(int argc, char **argv) {
                                 sizeof error)) {
         fprintf(stderr, "%s\n", error);
         return 1;
+    }
+    const char *dump = getenv("ENGINE_HOST_DUMP");
+    if (dump) {
+        FILE *f = fopen(dump, "wb");
+        if (!f || fwrite(plamo_model.logits, 4, plamo_model.vocab, f) != plamo_model.vocab ||
+            fwrite(plamo_model.state, 4, plamo_model.hidden, f) != plamo_model.hidden ||
+            fclose(f)) {
+            fprintf(stderr, "cannot write %s\n", dump);
+            return 1;
+        }
     }
     plamo_engine_get_info(e, &info);
     printf("{\"backend\": \"%s\", \"memory_mode\": \"%s\", ", info.backend, info.memory_mode);

@@ -7,7 +7,8 @@
  *     the same interface (runtime/tokenizer.h:9-17) takes its place: the
  *     vocabulary file holds the vocabulary size; direction 0 encodes the bytes
  *     alone, direction 1/2 wraps them in fixed translation prefix 0/1 and an
- *     end marker; ids decode to "<id>".
+ *     end marker; ids decode to "<id>". The two prefixes have the shape of
+ *     the reference's template prefixes (see toy_prefix).
  *   - runtime/resident.c (mach/mach.h), runtime/parallel.c (sys/qos.h,
  *     sysctl) and runtime/weight_cache.c (F_NOCACHE) are Darwin-only. With the
  *     GPU backend open the engine calls only the memory probes among them
@@ -27,8 +28,14 @@
 
 /* ---- tokenizer ---- */
 
-enum { TOY_FIRST_BYTE_ID = 32, TOY_END_ID = 17, TOY_MAX_IDS = 4096 + 64 };
-static const uint32_t toy_prefix[2][6] = {{20, 21, 22, 23, 24, 25}, {20, 21, 26, 27, 28, 29}};
+enum { TOY_FIRST_BYTE_ID = 32, TOY_END_ID = 17, TOY_MAX_IDS = 4096 + 64, TOY_PREFIX_IDS = 12 };
+/* The shape of the reference's translation prefixes (src/prompt.s:64-66 through
+ * runtime/tokenizer.c:178-184): bos, tag, "dataset", msg, "translation", tag,
+ * "input", key, "lang", val, the language, msg. Twelve ids that differ only in
+ * the language id at index 10 and end in the same id. */
+static const uint32_t toy_prefix[2][TOY_PREFIX_IDS] = {
+    {20, 21, 22, 23, 24, 21, 25, 26, 27, 28, 29, 23},
+    {20, 21, 22, 23, 24, 21, 25, 26, 27, 28, 30, 23}};
 
 struct plamo_tokenizer {
     uint64_t vocab;

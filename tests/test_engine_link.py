@@ -76,8 +76,14 @@ def test_tokenizer_only_engine_runs(engine_host, tmp_path):
     assert r.returncode == 0, r.stderr
     out = json.loads(r.stdout)
     assert out["memory_mode"] == "tokenizer"
-    # direction 1: prefix 0, the bytes, the end marker (host_stubs.c).
-    assert out["ids"] == [20, 21, 22, 23, 24, 25, 32 + ord("h") % 268, 32 + ord("i") % 268, 17]
+    # direction 1: prefix 0, the bytes, the end marker (host_stubs.c). The two
+    # prefixes have the template's shape: 12 ids, equal but for index 10.
+    prefix0 = [20, 21, 22, 23, 24, 21, 25, 26, 27, 28, 29, 23]
+    assert out["ids"] == prefix0 + [32 + ord("h") % 268, 32 + ord("i") % 268, 17]
+    r = run(engine_host, "tokenize", "2", "hi", env_extra={"PLAMO_MODEL_DIR": str(tmp_path)})
+    assert r.returncode == 0, r.stderr
+    ids = json.loads(r.stdout)["ids"]
+    assert ids[:10] == prefix0[:10] and ids[10] != prefix0[10] and ids[11] == prefix0[11]
     # No directory: the engine's own error names the profile (runtime/engine.c:40-44).
     r = run(engine_host, "tokenize", "0", "hi", env_extra={"PLAMO_MODEL_DIR": ""})
     assert r.returncode == 1

@@ -310,6 +310,48 @@ def test_prompt_prefix_cache_flows(pinned):
         s.close()
 
 
+@pytest.mark.parametrize("pinned", [False, True])
+def test_template_prefix_restore_after_prepare(pinned):
+    # The engine's prepare order with prefixes of the template's shape
+    # (tests/test_prompt_cache.py: 12 ids, equal but for index 10, same last
+    # id). After prepare the device holds prefix 1; a request in the other
+    # direction restores prefix 0 with every counter and layer 0's last rows
+    # unchanged, so only a full upload of the restored rows gives layer 0 the
+    # right language row. Then the other direction, and the first again.
+    from test_prompt_cache import TEMPLATE_PREFIXES
+    s = tiny(h=128, inter=257, dim=128, capacity=300, window=48, layers=3)
+    a, b = s.instance(pinned=pinned), s.instance()
+    be = plamo_hip.Backend(s)
+    try:
+        snaps = []
+        for ids in TEMPLATE_PREFIXES:
+            a.reset()
+            assert be.prefill(a, ids) == 1
+            snaps.append(prompt_cache.capture(a, ids))
+            assert snaps[-1] is not None
+        a.reset()
+        for n, direction in enumerate((0, 1, 0)):
+            ids = list(TEMPLATE_PREFIXES[direction]) + [(n * 5 + j * 3) % 17 for j in range(7)]
+            say(f"template prefix {direction} restored, request {n}")
+            a.reset()
+            b.reset()
+            assert prompt_cache.restore(snaps[direction], a, ids) == 12
+            assert be.prefill(a, ids[12:]) == 1
+            assert oracle_lib.prefill(b, ids)
+            compare(a, b)
+            for step in range(2):
+                token = prompt_cache.greedy(b)
+                assert be.forward(a, token) == 1
+                assert oracle_lib.forward(b, token)
+                compare(a, b)
+        clean(be)
+    finally:
+        be.close()
+        a.close()
+        b.close()
+        s.close()
+
+
 def test_decline_and_failure_contract():
     s = tiny(h=24, inter=40, dim=6, capacity=64)
     a = s.instance()
