@@ -128,10 +128,13 @@ int plamo_metal_linear(struct plamo_metal *, const struct plamo_matmul *);
  * a static device array of PLAMO_HIP_STATIC_SCRATCH_BYTES held by each GPU
  * until the process ends. Nothing is allocated. Rejected (0, reason in
  * info.note): tokens > 1 with 3 * round_up(tokens, 128) * columns * 2 bytes
- * of planes above PLAMO_HIP_STATIC_PLANE_BYTES, weights not resident, or no
- * static scratch on the device. Enqueued on the backend's stream; returns
- * after completion with the same bits as plamo_metal_linear. Calls that
- * overlap on one GPU (from any backend instance) share the array and race. */
+ * of planes above PLAMO_HIP_STATIC_PLANE_BYTES, weights not resident, no
+ * static scratch on the device, an input or output that is not device memory
+ * of the backend's GPU spanning every strided row, or a call that overlaps
+ * another on the same GPU (from any backend instance of the process: one
+ * call at a time owns the array, the other is refused). Enqueued on the
+ * backend's stream; returns after completion with the same bits as
+ * plamo_metal_linear. */
 #define PLAMO_HIP_STATIC_PLANE_BYTES (32ull << 20)
 #define PLAMO_HIP_STATIC_SCRATCH_BYTES ((64ull << 10) + (64ull << 20) + PLAMO_HIP_STATIC_PLANE_BYTES)
 int plamo_hip_linear_static(struct plamo_metal *, const struct plamo_matmul *);

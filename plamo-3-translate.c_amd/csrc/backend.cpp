@@ -21,6 +21,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <atomic>
 #include <chrono>
 #include <vector>
 
@@ -178,6 +179,9 @@ static_assert(kStaticCounterBytes + kStaticPartialBytes + PLAMO_HIP_STATIC_PLANE
 static __device__ __align__(256) unsigned char scratch[PLAMO_HIP_STATIC_SCRATCH_BYTES];
 constexpr int kMaxDevices = 64;
 static void *static_scratch[kMaxDevices];
+// One call at a time owns a GPU's scratch, whichever backend instance makes
+// it: a call that finds it taken is refused instead of sharing it.
+static std::atomic<bool> static_scratch_busy[kMaxDevices];
 
 namespace {
 
@@ -502,7 +506,18 @@ std::vector<uintptr_t> model_fingerprint(const struct model *model) {
 
 int prepare(plamo_metal *m, struct model *model) {
     std::vector<uintptr_t> f = model_fingerprint(model);
-    if (m->model == model && f == m->fingerprint) return 1;
+    if (m->model == model && f == m->fingerprint) {
+        // The fingerprint holds addresses only. A model rebuilt at the same
+        // addresses may have host arrays that are no longer pinned (or pinned
+        // anew): the direct-write views are checked on the state array (an
+        // instance's arrays are allocated alike) before kernels write them.
+        if (m->host_direct && device_view(model->state) != m->host_state) {
+            find_host_views(m, model);
+            for (Layer &l : m->layers) l.synced = false;
+            ++m->epoch;  // the captured graphs hold the old views
+        }
+        return 1;
+    }
     release_model(m);
     if (!model || !model->count || model->count > kMaxLayers || !model->hidden ||
         model->hidden > UINT32_MAX || !model->vocab || model->vocab > UINT32_MAX ||
@@ -1853,6 +1868,43 @@ int plamo_metal_linear(struct plamo_metal *m, const struct plamo_matmul *mm) {
     return 1;
 }
 
+namespace {
+
+// True when [p, p + bytes) lies inside one device allocation of this GPU
+// (hipMalloc memory). Host memory, pinned or not, and pointers the runtime
+// does not know are refused. Neither query allocates.
+bool device_extent(int device, const void *p, uint64_t bytes) {
+    hipPointerAttribute_t a{};
+    if (hipPointerGetAttributes(&a, p) != hipSuccess || a.type != hipMemoryTypeDevice ||
+        a.device != device) {
+        (void)hipGetLastError();
+        return false;
+    }
+    hipDeviceptr_t base = nullptr;
+    size_t size = 0;
+    if (hipMemGetAddressRange(&base, &size, (hipDeviceptr_t)p) != hipSuccess || !base) {
+        (void)hipGetLastError();
+        return false;
+    }
+    const uintptr_t b = (uintptr_t)base, q = (uintptr_t)p;
+    return q >= b && bytes <= size && q - b <= size - bytes;
+}
+
+struct ScratchOwner {
+    std::atomic<bool> *flag = nullptr;
+    bool take(int device) {
+        bool expected = false;
+        if (!static_scratch_busy[device].compare_exchange_strong(expected, true)) return false;
+        flag = &static_scratch_busy[device];
+        return true;
+    }
+    ~ScratchOwner() {
+        if (flag) flag->store(false);
+    }
+};
+
+}  // namespace
+
 int plamo_hip_linear_static(struct plamo_metal *m, const struct plamo_matmul *mm) {
     if (!m) return 0;
     if (!mm || !mm->input || !mm->output || !mm->rows || !mm->columns || !mm->tokens ||
@@ -1863,6 +1915,17 @@ int plamo_hip_linear_static(struct plamo_metal *m, const struct plamo_matmul *mm
     if (!w) return problem(m, "static linear: weights not resident");
     char *base = m->device < kMaxDevices ? (char *)static_scratch[m->device] : nullptr;
     if (!base) return problem(m, "static linear: no static scratch on this device");
+    // Kernels read the input and write the output directly: both must be
+    // device memory of this GPU spanning every row the strides reach (a host
+    // pointer would fault the GPU).
+    if (!device_extent(m->device, mm->input, ((T - 1) * mm->input_stride + K) * 4) ||
+        !device_extent(m->device, mm->output, ((T - 1) * mm->output_stride + N) * 4))
+        return problem(m, "static linear: input and output must be device memory of this GPU "
+                          "covering every strided row");
+    ScratchOwner owner;
+    if (!owner.take(m->device))
+        return problem(m, "static linear: the static scratch of this GPU is in use by another "
+                          "call");
     if (T > 1 && gemm_plane_elems(T, K) * 2 > PLAMO_HIP_STATIC_PLANE_BYTES)
         return problem(m,
                        "static linear: %llu tokens x %llu columns need %llu bytes of input "
@@ -1900,6 +1963,8 @@ int plamo_hip_linear_static(struct plamo_metal *m, const struct plamo_matmul *mm
     }
     ok = ok && end_timing(m);
     if (!ok) {
+        // Nothing of this call may still run when the scratch is released.
+        (void)hipStreamSynchronize(s);
         (void)hipGetLastError();
         return problem(m, "static linear: launch failed");
     }

@@ -2846,12 +2846,15 @@ __global__ __launch_bounds__(kAttnThreads) void decode_attention_kernel(DecodeAt
 // shares a CU's load path with an attention block's latency-bound loads.
 // (Rows per wave, C4 ms per step: 2: 3.114, 3: 3.089, 4: 3.053, 5: 3.060,
 // 6: 3.114.)
+// 8192-wide rows (16 chunks) take 2 rows per wave: 4 would hold 256 VGPRs
+// of weights per lane.
 constexpr int kORows = 4;
 constexpr size_t kAttentionOLds = 96 * 1024;
+__host__ __device__ constexpr int o_rows_per_wave(int kc) { return kc > 12 ? 2 : kORows; }
 
 template <int KC>
 __device__ __forceinline__ void oproj_block(const AttentionO &f, uint32_t ob) {
-    constexpr int U = kORows;
+    constexpr int U = o_rows_per_wave(KC);
     __shared__ int waited;
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const uint32_t r0 = (ob * kAttnWaves + wave) * U;
@@ -2907,7 +2910,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_o_kernel(AttentionO f)
 
 bool decode_attention_supported(uint32_t dim, uint32_t group) {
     return (dim == 64 || dim == 128) &&
-           (group == 1 || group == 2 || group == 4 || group == 6 || group == 8);
+           (group == 1 || group == 2 || group == 4 || group == 6 || group == 8 || group == 16);
 }
 
 uint32_t decode_attention_splits(uint64_t rows) {
@@ -2949,7 +2952,8 @@ static hipError_t decode_attention_dim(hipStream_t stream, const DecodeAttention
     case 2: return decode_attention_variant<DIM, 2>(stream, a);
     case 4: return decode_attention_variant<DIM, 4>(stream, a);
     case 6: return decode_attention_variant<DIM, 6>(stream, a);
-    default: return decode_attention_variant<DIM, 8>(stream, a);
+    case 8: return decode_attention_variant<DIM, 8>(stream, a);
+    default: return decode_attention_variant<DIM, 16>(stream, a);
     }
 }
 
@@ -2959,7 +2963,8 @@ static hipError_t attention_o_variant(hipStream_t stream, const AttentionO &f) {
     hipError_t e = hipFuncSetAttribute((const void *)attention_o_kernel<DIM, G, KC, ROWS>,
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return e;
-    const uint32_t oblocks = (f.rows + kORows * kAttnWaves - 1) / (kORows * kAttnWaves);
+    const uint32_t per_block = o_rows_per_wave(KC) * kAttnWaves;
+    const uint32_t oblocks = (f.rows + per_block - 1) / per_block;
     attention_o_kernel<DIM, G, KC, ROWS>
         <<<f.a.kh * f.a.splits + oblocks, kAttnThreads, lds, stream>>>(f);
     return hipGetLastError();
@@ -2976,8 +2981,10 @@ template <int DIM, int G>
 static hipError_t attention_o_cols(hipStream_t stream, const AttentionO &f) {
     switch (f.cols / 512) {
     case 4: return attention_o_rows<DIM, G, 4>(stream, f);
+    case 6: return attention_o_rows<DIM, G, 6>(stream, f);
     case 8: return attention_o_rows<DIM, G, 8>(stream, f);
-    default: return attention_o_rows<DIM, G, 12>(stream, f);
+    case 12: return attention_o_rows<DIM, G, 12>(stream, f);
+    default: return attention_o_rows<DIM, G, 16>(stream, f);
     }
 }
 
@@ -2988,13 +2995,14 @@ static hipError_t attention_o_dim(hipStream_t stream, const AttentionO &f) {
     case 2: return attention_o_cols<DIM, 2>(stream, f);
     case 4: return attention_o_cols<DIM, 4>(stream, f);
     case 6: return attention_o_cols<DIM, 6>(stream, f);
-    default: return attention_o_cols<DIM, 8>(stream, f);
+    case 8: return attention_o_cols<DIM, 8>(stream, f);
+    default: return attention_o_cols<DIM, 16>(stream, f);
     }
 }
 
 bool attention_o_supported(uint32_t dim, uint32_t group, uint64_t cols) {
     return decode_attention_supported(dim, group) &&
-           (cols == 2048 || cols == 4096 || cols == 6144);
+           (cols == 2048 || cols == 3072 || cols == 4096 || cols == 6144 || cols == 8192);
 }
 
 hipError_t launch_attention_o(hipStream_t stream, const AttentionO &f) {
@@ -3431,7 +3439,7 @@ __global__ __launch_bounds__(64 * G) void prompt_attention_mfma_kernel(PromptAtt
 static bool prompt_mfma_supported(uint32_t dim, uint32_t qh, uint32_t kh, uint32_t window) {
     if (window || !kh || qh % kh || (dim != 64 && dim != 128)) return false;
     const uint32_t g = qh / kh;
-    return g == 1 || g == 2 || g == 4 || g == 6 || g == 8;
+    return g == 1 || g == 2 || g == 4 || g == 6 || g == 8 || g == 16;
 }
 
 // Key splits of the matrix-core form: only when its blocks (one per KV head
@@ -3470,7 +3478,8 @@ static hipError_t prompt_mfma_dim(hipStream_t stream, const PromptAttention &a, 
     case 2: return prompt_mfma_variant<DIM, 2>(stream, a, splits, rows);
     case 4: return prompt_mfma_variant<DIM, 4>(stream, a, splits, rows);
     case 6: return prompt_mfma_variant<DIM, 6>(stream, a, splits, rows);
-    default: return prompt_mfma_variant<DIM, 8>(stream, a, splits, rows);
+    case 8: return prompt_mfma_variant<DIM, 8>(stream, a, splits, rows);
+    default: return prompt_mfma_variant<DIM, 16>(stream, a, splits, rows);
     }
 }
 

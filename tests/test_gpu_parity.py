@@ -440,6 +440,66 @@ def test_hooks_and_trampolines(hip):
         s.close()
 
 
+def test_compute_hooks_through_their_pointers(oracle):
+    # The reference's CPU layer calls the void matvec / matmul hooks and the
+    # 1/0 mlp hook through the pointers of runtime/compute.h:8-14 with
+    # plamo_compute_context as the last argument. Call them the same way.
+    s = tiny(h=128, inter=257, dim=128, capacity=64)
+    a = s.instance()
+    be = plamo_hip.Backend(s)
+    try:
+        ctx = ctypes.c_void_p(plamo_hip.hook_address("plamo_compute_context"))
+        assert ctx.value == be.handle
+        matvec_t = ctypes.CFUNCTYPE(None, plamo_hip.u16p, plamo_hip.f32p, plamo_hip.f32p,
+                                    ctypes.c_uint64, ctypes.c_uint64, ctypes.c_void_p)
+        matmul_t = ctypes.CFUNCTYPE(None, ctypes.POINTER(plamo_hip.Matmul), ctypes.c_void_p)
+        mlp_t = ctypes.CFUNCTYPE(ctypes.c_int, ctypes.POINTER(plamo_hip.Mlp), plamo_hip.f32p,
+                                 ctypes.c_uint64, ctypes.c_void_p)
+        matvec = matvec_t(plamo_hip.hook_address("plamo_matvec_kernel"))
+        matmul = matmul_t(plamo_hip.hook_address("plamo_matmul_kernel"))
+        mlp_hook = mlp_t(plamo_hip.hook_address("plamo_mlp_kernel"))
+        layer = a.layer(0)
+        q = layer.mixer.contents.qkv.contents
+        rows, cols = (q.qh + 2 * q.kh) * q.dim, q.hidden
+        rng = np.random.default_rng(4)
+        x = rng.standard_normal(cols).astype(np.float32)
+        y, ref = np.full(rows, np.nan, np.float32), np.zeros(rows, np.float32)
+        matvec(q.weight, x.ctypes.data_as(plamo_hip.f32p), y.ctypes.data_as(plamo_hip.f32p),
+               rows, cols, ctx)
+        oracle.oracle_matvec(q.weight, x.ctypes.data_as(plamo_hip.f32p),
+                             ref.ctypes.data_as(plamo_hip.f32p), ctypes.c_uint64(rows),
+                             ctypes.c_uint64(cols))
+        gate(y, ref, "matvec hook")
+        for tokens in (2, 24):
+            x = rng.standard_normal((tokens, cols + 3)).astype(np.float32)
+            y = np.full((tokens, rows + 5), np.nan, np.float32)
+            ref = np.zeros_like(y)
+            for out, call in ((y, lambda mm: matmul(ctypes.byref(mm), ctx)),
+                              (ref, lambda mm: oracle.oracle_matmul(ctypes.byref(mm)))):
+                call(plamo_hip.Matmul(q.weight, x.ctypes.data_as(plamo_hip.f32p),
+                                      out.ctypes.data_as(plamo_hip.f32p), rows, cols, tokens,
+                                      cols + 3, rows + 5))
+            gate(y[:, :rows], ref[:, :rows], f"matmul hook tokens={tokens}")
+            assert np.isnan(y[:, rows:]).all()  # the row padding is untouched
+        mlp = layer.mlp.contents
+        st = rng.standard_normal((3, 128)).astype(np.float32)
+        ref = st.copy()
+        assert mlp_hook(ctypes.byref(mlp), st.ctypes.data_as(plamo_hip.f32p), 3, ctx) == 1
+        for t in range(3):
+            row = ref[t].copy()
+            m2 = plamo_hip.Mlp(row.ctypes.data_as(plamo_hip.f32p), mlp.pre, mlp.post, mlp.gu,
+                               mlp.down, mlp.normalized, mlp.branch, mlp.scratch, 128,
+                               mlp.intermediate)
+            oracle.oracle_mlp_branch(ctypes.byref(m2))
+            ref[t] = row
+        gate(st, ref, "mlp hook")
+        clean(be)
+    finally:
+        be.close()
+        a.close()
+        s.close()
+
+
 def test_linear_and_mlp_entry_points(oracle):
     s = tiny(h=128, inter=257, dim=128, capacity=64)
     a = s.instance()

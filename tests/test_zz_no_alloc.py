@@ -96,9 +96,85 @@ def test_static_linear_matches_allocating_linear():
                               cols, 2, cols, rows)
         assert lib.plamo_hip_linear_static(be.handle, ctypes.byref(mm)) == 0
         assert b"not resident" in be.info().note
+        # Host memory (what plamo_metal_linear takes) is refused before any
+        # launch, as input and as output; so are strides that reach past the
+        # end of a device buffer.
+        host = np.zeros(2 * cols, np.float32)
+        hp = host.ctypes.data_as(plamo_hip.f32p)
+        small_x, small_y = DeviceArray(hip, 2 * cols), DeviceArray(hip, 2 * rows)
+        buffers += [small_x, small_y]
+        for x_, y_, xs_, ys_ in ((hp, small_y.f32p(), cols, rows),
+                                 (small_x.f32p(), hp, cols, rows),
+                                 (small_x.f32p(), small_y.f32p(), cols + 1, rows),
+                                 (small_x.f32p(), small_y.f32p(), cols, rows + 1)):
+            mm = plamo_hip.Matmul(q.weight, x_, y_, rows, cols, 2, xs_, ys_)
+            assert lib.plamo_hip_linear_static(be.handle, ctypes.byref(mm)) == 0
+            assert b"device memory" in be.info().note
+        mm = plamo_hip.Matmul(q.weight, small_x.f32p(), small_y.f32p(), rows, cols, 2, cols, rows)
+        assert lib.plamo_hip_linear_static(be.handle, ctypes.byref(mm)) == 1
     finally:
         for b in buffers:
             b.free()
         be.close()
+        inst.close()
+        s.close()
+
+
+def test_static_linear_calls_from_two_backends():
+    # Two backend instances of one process (a target and a draft) call the
+    # entry point from two threads at once. One call at a time owns the GPU's
+    # static scratch: every call either matches plamo_metal_linear bit for bit
+    # or is refused with a note; none sees the other's partial tiles.
+    import threading
+    lib = plamo_hip.load()
+    hip = ctypes.CDLL("libamdhip64.so.7")
+    s = plamo_hip.Synthetic(4096, 1, 32, 8, 128, 1024, 64, window=8, global_capacity=64,
+                            pattern=1, seed=37)
+    inst = s.instance()
+    backends = [plamo_hip.Backend(s), plamo_hip.Backend(s)]
+    buffers = []
+    try:
+        q = inst.layer(0).mixer.contents.qkv.contents
+        rows, cols, tokens = (q.qh + 2 * q.kh) * q.dim, q.hidden, 200
+        rng = np.random.default_rng(5)
+        jobs = []
+        for be in backends:
+            x = rng.standard_normal((tokens, cols)).astype(np.float32)
+            r, expected = be.linear(q.weight, x, rows)
+            assert r == 1
+            dx, dy = DeviceArray(hip, tokens * cols), DeviceArray(hip, tokens * rows)
+            buffers += [dx, dy]
+            dx.upload(x)
+            jobs.append((be, plamo_hip.Matmul(q.weight, dx.f32p(), dy.f32p(), rows, cols, tokens,
+                                              cols, rows), dy, expected))
+        outcomes = {"done": 0, "refused": 0}
+        for round_ in range(6):
+            results = [None, None]
+
+            def call(j):
+                be, mm, _, _ = jobs[j]
+                results[j] = lib.plamo_hip_linear_static(be.handle, ctypes.byref(mm))
+
+            threads = [threading.Thread(target=call, args=(j,)) for j in range(2)]
+            for t in threads:
+                t.start()
+            for t in threads:
+                t.join()
+            for j, (be, _, dy, expected) in enumerate(jobs):
+                if results[j] == 1:
+                    got = dy.download(tokens * rows).reshape(tokens, rows)
+                    assert got.tobytes() == expected.tobytes(), f"round {round_} backend {j}"
+                    outcomes["done"] += 1
+                else:
+                    assert b"in use by another call" in be.info().note
+                    outcomes["refused"] += 1
+                dy.upload(np.full(tokens * rows, np.nan, np.float32))
+        say(f"static linear from two threads: {outcomes}")
+        assert outcomes["done"] >= 6
+    finally:
+        for b in buffers:
+            b.free()
+        for be in backends:
+            be.close()
         inst.close()
         s.close()
