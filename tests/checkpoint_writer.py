@@ -62,19 +62,25 @@ def weights(syn: "plamo_hip.Synthetic") -> list[tuple[str, np.ndarray]]:
         inst.close()
 
 
-def safetensors_bytes(tensors, metadata=None, dtype="BF16") -> bytes:
-    header, blobs, offset = {}, [], 0
+def safetensors_header(tensors, metadata=None, dtype="BF16") -> bytes:
+    """The length prefix and the padded JSON header of a safetensors file
+    holding `tensors` in order."""
+    header, offset = {}, 0
     if metadata is not None:
         header["__metadata__"] = metadata
     for name, a in tensors:
-        raw = np.ascontiguousarray(a).tobytes()
+        size = a.size * a.itemsize
         header[name] = {"dtype": dtype, "shape": list(a.shape),
-                        "data_offsets": [offset, offset + len(raw)]}
-        blobs.append(raw)
-        offset += len(raw)
+                        "data_offsets": [offset, offset + size]}
+        offset += size
     text = json.dumps(header, separators=(",", ":")).encode()
     text += b" " * (-len(text) % 8)
-    return struct.pack("<Q", len(text)) + text + b"".join(blobs)
+    return struct.pack("<Q", len(text)) + text
+
+
+def safetensors_bytes(tensors, metadata=None, dtype="BF16") -> bytes:
+    return safetensors_header(tensors, metadata, dtype) + b"".join(
+        np.ascontiguousarray(a).tobytes() for _, a in tensors)
 
 
 def config(syn: "plamo_hip.Synthetic", max_positions: int | None = None) -> dict:
@@ -119,6 +125,10 @@ def write(directory: Path, syn: "plamo_hip.Synthetic", shards: int = 2,
     tensors = weights(syn)
     for s in range(shards):
         part = tensors[s::shards]
-        (directory / f"model-{s + 1:05d}-of-{shards:05d}.safetensors").write_bytes(
-            safetensors_bytes(part, metadata={"format": "pt"}))
+        # Streamed tensor by tensor: no whole-file buffer (a 0.8B-profile
+        # checkpoint is 1.7 GB).
+        with open(directory / f"model-{s + 1:05d}-of-{shards:05d}.safetensors", "wb") as f:
+            f.write(safetensors_header(part, metadata={"format": "pt"}))
+            for _, a in part:
+                f.write(memoryview(np.ascontiguousarray(a)).cast("B"))
     return directory
