@@ -117,6 +117,52 @@ def host_threads() -> tuple[int, int]:
     return max(1, share), nproc
 
 
+def smaller_config_baseline(lib, name: str, threads: int) -> dict:
+    """C2 / C3 on the C oracle (decode s/step and the
+    128-token prefill, at N threads and at 1 thread). The whole 128-token
+    prompt is prefilled at N threads; at 1 thread its first two layers are,
+    scaled by the layer count. Decode steps follow the prompt greedily: three
+    at N threads, one at 1 thread."""
+    c = dict(plamo_hip.CONFIGS[name])
+    syn = plamo_hip.Synthetic(**c, seed=20261202, threads=threads)
+    inst = syn.instance()
+    try:
+        prompt = np.random.default_rng(11).integers(0, c["vocab"], size=128).astype(np.uint32)
+        ids = (ctypes.c_uint32 * 128)(*prompt.tolist())
+
+        def prefill(n_threads, layers):
+            inst.reset()
+            view = plamo_hip.Model.from_buffer_copy(inst.model)
+            view.count = layers
+            lib.oracle_set_threads(n_threads)
+            start = time.perf_counter()
+            if not lib.oracle_prefill(ctypes.byref(view), ids, 128, None):
+                raise RuntimeError(f"{name}: oracle prefill failed")
+            return time.perf_counter() - start
+
+        L = c["layers"]
+        p_1 = prefill(1, 2) * L / 2
+        p_n = prefill(threads, L)
+        token = int(lib.oracle_argmax(inst.model.logits, inst.model.vocab))
+        step = {}
+        for n_threads, count in ((threads, 3), (1, 1)):
+            lib.oracle_set_threads(n_threads)
+            start = time.perf_counter()
+            for _ in range(count):
+                if not lib.oracle_forward(inst.model_ptr, token):
+                    raise RuntimeError(f"{name}: oracle decode failed")
+                token = int(lib.oracle_argmax(inst.model.logits, inst.model.vocab))
+            step[str(n_threads)] = round((time.perf_counter() - start) / count, 4)
+        return {"decode_s_per_step": step,
+                "prefill_128_s": {str(threads): round(p_n, 3), "1": round(p_1, 2)},
+                "sample": f"128-token prompt: all {L} layers at {threads} threads, 2 of {L} at "
+                          f"1 thread scaled; decode: 3 steps at {threads} threads, 1 at 1 "
+                          f"thread"}
+    finally:
+        inst.close()
+        syn.close()
+
+
 def cpu_baseline(inst: plamo_hip.Instance, token: int, seconds: float, cfg: dict, prompt,
                  snap) -> dict:
     """The C oracle on the host cores, on bounded
@@ -189,10 +235,13 @@ def cpu_baseline(inst: plamo_hip.Instance, token: int, seconds: float, cfg: dict
     sample_n = min(L, 4)
     p_n = prefill(threads, sample_n)
     p_1 = prefill(1, 1)
+    smaller = {name: smaller_config_baseline(lib, name, threads)
+               for name in ("c2", "c3") if name != cfg["name"]}
     return {"value": steps_n / t_n, "unit": "tok/s", "cores": threads, "kind": "port",
             "nproc": nproc,
             "one_thread_tok_s": steps_1 / t_1,
             "c1_layer_step_ms": layer_ms,
+            **{f"{name}": v for name, v in smaller.items()},
             "prefill_128_s": {str(threads): round(p_n * L / sample_n, 2),
                               "1": round(p_1 * L, 2),
                               "measured": f"{sample_n} of {L} layers at {threads} threads "
