@@ -123,6 +123,8 @@ struct plamo_metal {
     float *state_a = nullptr, *state_b = nullptr, *qkv = nullptr, *q = nullptr, *attn = nullptr,
           *branch = nullptr, *act = nullptr, *down_out = nullptr, *partial = nullptr;
     uint32_t *counters = nullptr;
+    uint32_t *attention_flags = nullptr;  // [layers][kAttentionFlags] step tags
+    uint32_t step_tag = 0;                // last decode step's tag
     float *outbox = nullptr, *outbox_host = nullptr;  // logits | state | normalized | stage
     uint64_t outbox_floats = 0;
     // When every host array a step updates is pinned and device-visible, the
@@ -651,6 +653,7 @@ int prepare(plamo_metal *m, struct model *model) {
     dev_free(m, m->down_out);
     dev_free(m, m->partial);
     dev_free(m, m->counters);
+    dev_free(m, m->attention_flags);
     dev_free(m, m->outbox);
     if (m->outbox_host) (void)hipHostFree(m->outbox_host);
     m->outbox_host = nullptr;
@@ -664,13 +667,15 @@ int prepare(plamo_metal *m, struct model *model) {
     m->down_out = dev_alloc<float>(m, h);
     m->partial = dev_alloc<float>(m, m->max_partial * m->max_splits);
     m->counters = dev_alloc<uint32_t>(m, 256);
+    m->attention_flags = dev_alloc<uint32_t>(m, L * kAttentionFlags);
     m->outbox_floats = V + 2 * h + L * 3 * m->max_width;
     m->outbox = dev_alloc<float>(m, m->outbox_floats);
     if (!m->state_a || !m->state_b || !m->qkv || !m->q || !m->attn || !m->branch || !m->act ||
-        !m->down_out || !m->partial || !m->counters || !m->outbox ||
+        !m->down_out || !m->partial || !m->counters || !m->attention_flags || !m->outbox ||
         hipHostMalloc((void **)&m->outbox_host, m->outbox_floats * 4, hipHostMallocDefault) !=
             hipSuccess ||
-        hipMemset(m->counters, 0, 256 * 4) != hipSuccess) {
+        hipMemset(m->counters, 0, 256 * 4) != hipSuccess ||
+        hipMemset(m->attention_flags, 0, L * kAttentionFlags * 4) != hipSuccess) {
         (void)hipGetLastError();
         release_model(m);
         return problem(m, "cannot allocate decode workspace");
@@ -886,6 +891,7 @@ int encode_decode(plamo_metal *m, struct model *model, const DecodePlan &plan, i
                 ao.heads = d.kh;
                 ao.done = m->params_dev->done + i;
                 ao.error = &m->params_dev->error;
+                ao.flags = m->attention_flags + i * kAttentionFlags;
                 HIP_TRY(m, launch_attention_o(s, ao));
                 fused_o = true;
             } else {
@@ -1260,6 +1266,9 @@ int plamo_metal_forward(struct plamo_metal *m, struct model *model, uint64_t tok
     if (plan.special && (!ensure_prompt(m, model, 1) || !ensure_window_scratch(m, model))) return -1;
     m->params_host->token = (uint32_t)token;
     m->params_host->tokens = 1;
+    // A fresh tag per step (never 0, the flags' initial value).
+    if (++m->step_tag == 0) m->step_tag = 1;
+    m->params_host->step = m->step_tag;
     *m->status_host = 0;
     plan.direct = m->host_direct && !plan.special;
     bool short_ctx = true;

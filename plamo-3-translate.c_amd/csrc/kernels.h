@@ -24,6 +24,9 @@ struct StepParams {
     // Both are zero outside tests, which raise them from the host so that a
     // wait gives up and the failure path runs with every kernel exiting.
     uint32_t wait_extra, wait_limit;
+    // Nonzero tag of this decode step, new for every step of a backend: the
+    // fused attention's blocks publish it in their completion flags.
+    uint32_t step;
 };
 
 // Norm applied in a GEMV prologue: x = rms(src) * (bf16(w) + offset).
@@ -186,13 +189,20 @@ struct AttentionO {
     uint32_t rows, cols, heads;
     uint32_t *done;
     uint32_t *error;
+    // Per attention block of this layer, the step tag of its last completed
+    // partial (kAttentionFlags words, zero when allocated): up to
+    // kDecodeShortRows allocated rows the O blocks wait on these instead of
+    // `done`.
+    uint32_t *flags;
 };
+constexpr uint32_t kAttentionFlags = 64;
 hipError_t launch_attention_o(hipStream_t, const AttentionO &);
 bool attention_o_supported(uint32_t dim, uint32_t group, uint64_t cols);
 // Blocks per KV head that cover `rows` cache rows (DecodeAttention::splits
 // must be at least this for the largest row count of the launch).
 // Allocated rows up to which the decode attention uses its short-context
-// blocks (32 rows each); a decode step whose rows all stay below it may cap
+// blocks (32 rows each; 64 in the fused attention + O launch, whose O blocks
+// merge the partials); a decode step whose rows all stay below it may cap
 // the attention's view of the allocation here.
 constexpr uint32_t kDecodeShortRows = 256;
 uint32_t decode_attention_splits(uint64_t rows);

@@ -155,6 +155,34 @@ __device__ __forceinline__ bool block_wait(const uint32_t *counter, uint32_t tar
     return *flag;
 }
 
+// Bounded wait until flags[0, n) all hold `tag`, for a whole block: wave 0
+// polls (one load per lane and poll) while the other waves wait at the
+// barrier. Each flag has one writer, so no arrival contends for an address.
+// Returns false when the wait gave up after `limit` polls; call from every
+// thread of the block.
+__device__ __forceinline__ bool flags_wait(const uint32_t *flags, uint32_t n, uint32_t tag,
+                                           uint32_t limit, int *flag) {
+    if (threadIdx.x < 64) {
+        bool ok = true;
+        for (uint32_t spins = 0;;) {
+            bool mine = true;
+            for (uint32_t b = threadIdx.x; b < n; b += 64)
+                mine = mine && __hip_atomic_load(const_cast<uint32_t *>(flags + b),
+                                                 __ATOMIC_RELAXED,
+                                                 __HIP_MEMORY_SCOPE_AGENT) == tag;
+            if (__builtin_amdgcn_ballot_w64(!mine) == 0) break;
+            __builtin_amdgcn_s_sleep(2);
+            if (++spins >= limit) {
+                ok = false;
+                break;
+            }
+        }
+        if (threadIdx.x == 0) *flag = ok;
+    }
+    __syncthreads();
+    return *flag;
+}
+
 // The device's own status for the host: block 0 of a launch that carries a
 // Prologue with `status_out` copies the step's error word there (the decode
 // head, a pinned host word), so a step whose bounded wait gave up is reported
@@ -2439,7 +2467,7 @@ __host__ __device__ constexpr uint32_t attention_rows(uint64_t rows) {
 // One attention block (KV head kvh, row split `split`). With `done`, the block
 // that completes a KV head's output writes it through to the coherence point
 // and counts the head in *done (the fused O projection waits on it).
-template <int DIM, int G, int W, int ROWS>
+template <int DIM, int G, int W, int ROWS, bool OM = false>
 __device__ __forceinline__ void attention_block(const DecodeAttention &a, uint32_t kvh,
                                                 uint32_t split, uint32_t *done) {
     constexpr uint32_t RW = ROWS / W;  // rows per wave
@@ -2753,6 +2781,27 @@ __device__ __forceinline__ void attention_block(const DecodeAttention &a, uint32
 #pragma unroll
         for (int e = 0; e < PL; ++e) wpart[(wave * G + g) * DIM + lane * PL + e] = acc[g][e];
     __syncthreads();
+    if (OM) {
+        // Unnormalized partial of this split for the O blocks to merge:
+        // values [split][qh][DIM], then (maximum, sum) [split][qh][2].
+        float *stats_out = a.partial + (uint64_t)a.splits * a.qh * DIM;
+        for (uint32_t i = threadIdx.x; i < G * DIM; i += W * 64) {
+            const uint32_t g = i / DIM, d = i % DIM;
+            float o = 0.0f;
+#pragma unroll
+            for (uint32_t w = 0; w < (uint32_t)W; ++w) o = o + wpart[(w * G + g) * DIM + d];
+            const uint64_t head = (uint64_t)split * a.qh + kvh * G + g;
+            store_through(a.partial + head * DIM + d, o);
+            if (d < 2) store_through(stats_out + head * 2 + d, stats[g][d]);
+        }
+        // `done` is this block's flag here: the step's tag once every store
+        // of the partial has completed.
+        wait_stores();
+        __syncthreads();
+        if (threadIdx.x == 0)
+            __hip_atomic_store(done, a.params->step, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return;
+    }
     for (uint32_t i = threadIdx.x; i < G * DIM; i += W * 64) {
         const uint32_t g = i / DIM, d = i % DIM;
         float o = 0.0f;
@@ -2852,10 +2901,65 @@ constexpr int kORows = 4;
 constexpr size_t kAttentionOLds = 96 * 1024;
 __host__ __device__ constexpr int o_rows_per_wave(int kc) { return kc > 12 ? 2 : kORows; }
 
-template <int KC>
+// Rows per attention block when the O blocks merge the partials (OM): at
+// most kDecodeShortRows / kMergeRows splits per KV head.
+constexpr uint32_t kMergeRows = 64, kOMergeSplits = kDecodeShortRows / kMergeRows;
+
+// The attention output for the O blocks of an OM launch: every thread of the
+// block merges 8-column segments of the split partials (the merge of
+// attention_block: maximum, exp rescale, FMA sums in split order, divide) into
+// LDS. Partials were written through and counted before the wait ended, and
+// no block of this launch read them earlier, so plain loads see them.
+template <int DIM>
+__device__ __forceinline__ void merge_partials(const AttentionO &f, uint32_t live, float *xs) {
+    const float *vals = f.a.partial;
+    const float *stats = f.a.partial + (uint64_t)f.a.splits * f.a.qh * DIM;
+    for (uint32_t seg = threadIdx.x; seg < f.cols / 8; seg += kAttnThreads) {
+        const uint32_t col = seg * 8, hq = col / DIM, d0 = col % DIM;
+        float m[kOMergeSplits], l[kOMergeSplits], v[kOMergeSplits][8];
+#pragma unroll
+        for (uint32_t sI = 0; sI < kOMergeSplits; ++sI) {
+            if (sI >= f.a.splits) break;
+            const uint64_t head = (uint64_t)sI * f.a.qh + hq;
+            const f32x2 ml = *(const f32x2 *)(stats + head * 2);
+            const f32x4 a = *(const f32x4 *)(vals + head * DIM + d0);
+            const f32x4 b = *(const f32x4 *)(vals + head * DIM + d0 + 4);
+            m[sI] = ml.x;
+            l[sI] = ml.y;
+            v[sI][0] = a.x; v[sI][1] = a.y; v[sI][2] = a.z; v[sI][3] = a.w;
+            v[sI][4] = b.x; v[sI][5] = b.y; v[sI][6] = b.z; v[sI][7] = b.w;
+        }
+        float out[8];
+        if (live == 1) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) out[e] = v[0][e] / l[0];
+        } else {
+            float mx = -__builtin_inff(), sum = 0.0f, o[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+            for (uint32_t sI = 0; sI < kOMergeSplits; ++sI)
+                if (sI < live) mx = fmaxf(mx, m[sI]);
+#pragma unroll
+            for (uint32_t sI = 0; sI < kOMergeSplits; ++sI) {
+                if (sI >= live) break;
+                const float fs = plamo_exp(m[sI] - mx);
+                sum = __builtin_fmaf(l[sI], fs, sum);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) o[e] = __builtin_fmaf(v[sI][e], fs, o[e]);
+            }
+#pragma unroll
+            for (int e = 0; e < 8; ++e) out[e] = o[e] / sum;
+        }
+        *(f32x4 *)(xs + col) = f32x4{out[0], out[1], out[2], out[3]};
+        *(f32x4 *)(xs + col + 4) = f32x4{out[4], out[5], out[6], out[7]};
+    }
+    __syncthreads();
+}
+
+template <int KC, int DIM = 128, bool OM = false>
 __device__ __forceinline__ void oproj_block(const AttentionO &f, uint32_t ob) {
     constexpr int U = o_rows_per_wave(KC);
     __shared__ int waited;
+    extern __shared__ __attribute__((aligned(16))) float xs[];
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const uint32_t r0 = (ob * kAttnWaves + wave) * U;
     if (ob * kAttnWaves * U >= f.rows) return;  // block-uniform: the wait below is block-wide
@@ -2870,14 +2974,33 @@ __device__ __forceinline__ void oproj_block(const AttentionO &f, uint32_t ob) {
     // Zero in the step's parameters means: wait for every KV head, up to
     // 2^22 polls. Other values exist for tests, which raise the target past
     // the heads so that the wait gives up while every block still exits.
-    const uint32_t limit = f.a.params->wait_limit ? f.a.params->wait_limit : (1u << 22);
-    const bool ok = block_wait(f.done, f.heads + f.a.params->wait_extra, limit, &waited);
+    // Every wave holds its weight rows before it reads the step's parameters
+    // and joins the wait. Reading them while the weights are in flight (as
+    // scalar loads, or as agent-scope vector loads) measured 0.6-0.9 us per
+    // C4 layer slower.
+    __builtin_amdgcn_s_waitcnt(0);
+    const uint32_t wait_limit = f.a.params->wait_limit;
+    const uint32_t wait_extra = f.a.params->wait_extra;
+    const uint32_t step = OM ? f.a.params->step : 0;
+    const uint32_t count = OM ? f.a.params->count[f.a.layer] : 0;
+    const uint32_t limit = wait_limit ? wait_limit : (1u << 22);
+    bool ok;
+    if (OM) {
+        // The live splits' blocks (the first kh * live of the launch) have
+        // published this step's tag; a nonzero wait_extra asks for a tag no
+        // block writes.
+        const uint32_t live = (count + kMergeRows) / kMergeRows;
+        ok = flags_wait(f.flags, f.a.kh * live, step + wait_extra, limit, &waited);
+        merge_partials<DIM>(f, live, xs);
+    } else {
+        ok = block_wait(f.done, f.heads + wait_extra, limit, &waited);
+    }
     float acc[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) acc[u] = 0.0f;
 #pragma unroll
     for (int c = 0; c < KC; ++c) {
-        const f32x4 *xp = (const f32x4 *)(f.x + c * 512 + lane * 8);
+        const f32x4 *xp = (const f32x4 *)((OM ? xs : f.x) + c * 512 + lane * 8);
         const f32x4 x0 = xp[0], x1 = xp[1];
         const float x[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
 #pragma unroll
@@ -2898,14 +3021,15 @@ __device__ __forceinline__ void oproj_block(const AttentionO &f, uint32_t ob) {
     if (!ok && threadIdx.x == 0) atomicOr(f.error, 1u);
 }
 
-template <int DIM, int G, int KC, int ROWS>
+template <int DIM, int G, int KC, int ROWS, bool OM = false>
 __global__ __launch_bounds__(kAttnThreads) void attention_o_kernel(AttentionO f) {
     const uint32_t attention_blocks = f.a.kh * f.a.splits;
     if (blockIdx.x < attention_blocks)
-        attention_block<DIM, G, kAttnWaves, ROWS>(f.a, blockIdx.x % f.a.kh, blockIdx.x / f.a.kh,
-                                                  f.done);
+        attention_block<DIM, G, kAttnWaves, ROWS, OM>(f.a, blockIdx.x % f.a.kh,
+                                                      blockIdx.x / f.a.kh,
+                                                      OM ? f.flags + blockIdx.x : f.done);
     else
-        oproj_block<KC>(f, blockIdx.x - attention_blocks);
+        oproj_block<KC, DIM, OM>(f, blockIdx.x - attention_blocks);
 }
 
 bool decode_attention_supported(uint32_t dim, uint32_t group) {
@@ -2957,24 +3081,31 @@ static hipError_t decode_attention_dim(hipStream_t stream, const DecodeAttention
     }
 }
 
-template <int DIM, int G, int KC, int ROWS>
+template <int DIM, int G, int KC, int ROWS, bool OM = false>
 static hipError_t attention_o_variant(hipStream_t stream, const AttentionO &f) {
     const size_t lds = std::max(decode_attention_lds(DIM, G, ROWS), kAttentionOLds);
-    hipError_t e = hipFuncSetAttribute((const void *)attention_o_kernel<DIM, G, KC, ROWS>,
+    hipError_t e = hipFuncSetAttribute((const void *)attention_o_kernel<DIM, G, KC, ROWS, OM>,
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return e;
     const uint32_t per_block = o_rows_per_wave(KC) * kAttnWaves;
     const uint32_t oblocks = (f.rows + per_block - 1) / per_block;
-    attention_o_kernel<DIM, G, KC, ROWS>
+    attention_o_kernel<DIM, G, KC, ROWS, OM>
         <<<f.a.kh * f.a.splits + oblocks, kAttnThreads, lds, stream>>>(f);
     return hipGetLastError();
 }
 
+// Up to kDecodeShortRows allocated rows the O blocks merge the partials of
+// kMergeRows-row attention blocks (no merging attention block, no second
+// hand-off); beyond, the last attention block of each KV head merges them.
 template <int DIM, int G, int KC>
 static hipError_t attention_o_rows(hipStream_t stream, const AttentionO &f) {
-    return attention_rows(f.a.rows) == kShortRows
-               ? attention_o_variant<DIM, G, KC, kShortRows>(stream, f)
-               : attention_o_variant<DIM, G, KC, kRowsPerBlock>(stream, f);
+    if (f.a.rows <= kDecodeShortRows && f.flags &&
+        f.a.kh * ((f.a.rows + kMergeRows - 1) / kMergeRows) <= kAttentionFlags) {
+        AttentionO m = f;
+        m.a.splits = (f.a.rows + kMergeRows - 1) / kMergeRows;
+        return attention_o_variant<DIM, G, KC, kMergeRows, true>(stream, m);
+    }
+    return attention_o_variant<DIM, G, KC, kRowsPerBlock>(stream, f);
 }
 
 template <int DIM, int G>
