@@ -151,6 +151,8 @@ struct plamo_metal {
     uint32_t *v_next = nullptr, *v_next_host = nullptr;
     void *v_argmax = nullptr;  // argmax partials of the candidate logits
     CopyRow *copy_table = nullptr, *copy_table_host = nullptr;
+    CopyRow *upload_table = nullptr;  // pinned: host-to-device rows of sync_from_host
+    const CopyRow *upload_view = nullptr;  // its device view
     uint64_t verification_tokens = 0, verification_index = 0;
 
     Buffer lin_in, lin_out, mlp_state, mlp_norm, mlp_gu, mlp_act, mlp_branch, mlp_norms;
@@ -725,9 +727,15 @@ constexpr uint64_t kPromptPrefixLimit = 64;
 // depends only on its token, so the sampled last rows agree too. So at prompt
 // entry (`prompt_entry`) a layer whose host count is a prefix length
 // (1..PLAMO_PROMPT_PREFIX_LIMIT) is always uploaded in full.
+//
+// When the host arrays are device-visible (pinned), the uploads run as one
+// copy kernel reading them through their device views: a restored prefix is
+// 3 arrays x layers segments, and as many DMA copies cost ~0.9 ms of a C4
+// 128-token TTFT against ~0.1 ms for the kernel.
 int sync_from_host(plamo_metal *m, struct model *model, std::vector<char> &stale,
                    bool prompt_entry) {
     stale.assign(model->count, 0);
+    uint32_t entries = 0;
     for (uint64_t i = 0; i < model->count; ++i) {
         Layer &d = m->layers[i];
         const struct mixer *mx = model->layers[i]->mixer;
@@ -746,17 +754,25 @@ int sync_from_host(plamo_metal *m, struct model *model, std::vector<char> &stale
             continue;
         }
         if (!ensure_kv_rows(m, d, c->count)) return 0;
-        uint64_t bytes = c->count * c->width * 4;
-        if (bytes) {
+        const uint64_t floats = c->count * c->width, bytes = floats * 4;
+        const bool rotated = r->processed_count == c->count && r->scale_bits == scale;
+        const bool viewed = m->host_direct && d.host_k && d.host_v && d.host_rot;
+        if (bytes && viewed) {
+            m->upload_table[entries++] = CopyRow{d.host_k, d.k, floats};
+            m->upload_table[entries++] = CopyRow{d.host_v, d.v, floats};
+            if (rotated) m->upload_table[entries++] = CopyRow{d.host_rot, d.rot, floats};
+        } else if (bytes) {
             HIP_TRY(m, hipMemcpyAsync(d.k, c->k, bytes, hipMemcpyHostToDevice, m->stream));
             HIP_TRY(m, hipMemcpyAsync(d.v, c->v, bytes, hipMemcpyHostToDevice, m->stream));
+            if (rotated)
+                HIP_TRY(m, hipMemcpyAsync(d.rot, r->out, bytes, hipMemcpyHostToDevice, m->stream));
         }
-        bool rotated = r->processed_count == c->count && r->scale_bits == scale;
-        if (rotated && bytes)
-            HIP_TRY(m, hipMemcpyAsync(d.rot, r->out, bytes, hipMemcpyHostToDevice, m->stream));
         stale[i] = !rotated && c->count;
         d.synced = false;
     }
+    // The kernel reads the table on the stream; the previous call's upload has
+    // completed, since every call waits for its work.
+    HIP_TRY(m, launch_copy_rows(m->stream, m->upload_view, entries));
     return 1;
 }
 
@@ -1142,6 +1158,9 @@ struct plamo_metal *plamo_metal_open(const struct plamo_metal_config *config, ch
         !(m->params_view = (StepParams *)device_view(m->params_host)) ||
         hipHostMalloc((void **)&m->status_host, 64, hipHostMallocDefault) != hipSuccess ||
         !(m->status_dev = (uint32_t *)device_view(m->status_host)) ||
+        hipHostMalloc((void **)&m->upload_table, 3 * kMaxLayers * sizeof(CopyRow),
+                      hipHostMallocDefault) != hipSuccess ||
+        !(m->upload_view = (const CopyRow *)device_view(m->upload_table)) ||
         hipMalloc((void **)&m->params_dev, sizeof(StepParams)) != hipSuccess) {
         (void)hipGetLastError();
         if (error && cap) snprintf(error, cap, "cannot create HIP stream or staging");
@@ -1201,6 +1220,7 @@ void plamo_metal_close(struct plamo_metal *m) {
     if (m->copy_table_host) (void)hipHostFree(m->copy_table_host);
     if (m->params_host) (void)hipHostFree(m->params_host);
     if (m->status_host) (void)hipHostFree(m->status_host);
+    if (m->upload_table) (void)hipHostFree(m->upload_table);
     if (m->params_dev) (void)hipFree(m->params_dev);
     if (m->start) (void)hipEventDestroy(m->start);
     if (m->stop) (void)hipEventDestroy(m->stop);
