@@ -1510,6 +1510,10 @@ int run_prompt(plamo_metal *m, struct model *model, const uint32_t *ids, uint64_
         }
         HIP_FAIL(m, launch_qkv_post(s, qp));
         ++n;
+        // With states == NULL only the final row feeds the logits; the last
+        // layer's projection and MLP run for that row alone
+        // (runtime/metal_model.m:761-770).
+        const bool last_row_only = !verify && !states && i + 1 == L && T > 1;
         PromptAttention pa{};
         pa.q = q;
         pa.table = rope.table;
@@ -1520,6 +1524,15 @@ int run_prompt(plamo_metal *m, struct model *model, const uint32_t *ids, uint64_
         pa.qh = d.qh;
         pa.kh = d.kh;
         pa.dim = d.dim;
+        // The O projection over every row reads the attention output as BF16
+        // planes, written by the attention itself.
+        const uint32_t o_tp =
+            !last_row_only && !overflow[i] &&
+                    prompt_attention_writes_planes(d.dim, d.qh, d.kh, 0)
+                ? gemm_planes_rows(T, aw, ws)
+                : 0;
+        pa.planes = o_tp ? planes : nullptr;
+        pa.padded = o_tp;
         if (overflow[i]) {
             pa.k_cache = d.k;
             pa.v_cache = d.v;
@@ -1561,11 +1574,8 @@ int run_prompt(plamo_metal *m, struct model *model, const uint32_t *ids, uint64_
                                        d.rot + rot_first * d.width, (end - rot_first) * w,
                                        hipMemcpyDeviceToHost, m->copy_stream));
         }
-        // With states == NULL only the final row feeds the logits; the last
-        // layer's projection and MLP run for that row alone
-        // (runtime/metal_model.m:761-770).
         uint64_t first = 0, rows = T;
-        if (!verify && !states && i + 1 == L && T > 1) {
+        if (last_row_only) {
             first = T - 1;
             rows = 1;
         }
@@ -1589,7 +1599,8 @@ int run_prompt(plamo_metal *m, struct model *model, const uint32_t *ids, uint64_
             HIP_FAIL(m, launch_residual_rows(s, st, branch, mpost, kMlpOffset, h, 1));
             n += 5;
         } else {
-            HIP_FAIL(m, launch_gemm(s, attn + first * aw, aw, d.o, h, aw, rows, branch, h, ws));
+            HIP_FAIL(m, launch_gemm(s, attn + first * aw, aw, d.o, h, aw, rows, branch, h, ws,
+                                    o_tp != 0));
             bool gu_planes = false;
             if (fuse_rows) {
                 const uint32_t tp = gemm_planes_rows(rows, h, ws);

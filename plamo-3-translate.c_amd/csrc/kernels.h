@@ -93,8 +93,9 @@ uint64_t gemm_plane_elems(uint64_t tokens, uint64_t cols);
 // multiple of 64: BF16 matrix cores on the exact three-term split of X; else
 // FP32 MFMA with BF16 weights widened in LDS.
 // planes_ready: the BF16 planes of X for the matrix-core path are already in
-// ws->planes (written by launch_norm_rows / launch_residual_norm_rows with
-// gemm_planes_rows(tokens, cols, ws) rows); other paths read x as usual.
+// ws->planes (written by launch_norm_rows / launch_residual_norm_rows /
+// launch_swiglu_rows / launch_prompt_attention with gemm_planes_rows(tokens,
+// cols, ws) rows), and x is not read; other paths read x as usual.
 hipError_t launch_gemm(hipStream_t, const float *x, uint64_t x_stride, const uint16_t *w,
                        uint64_t rows, uint64_t cols, uint64_t tokens, float *y,
                        uint64_t y_stride, const GemmWorkspace *ws, bool planes_ready = false);
@@ -221,8 +222,17 @@ struct PromptAttention {
     // Optional scratch for key splits (prompt_attention_scratch floats): few
     // query tiles then spread their keys over several blocks and a merge.
     float *partial;
+    // Optional: the output rows as launch_gemm's BF16 planes (rows padded to
+    // `padded`) instead of FP32 rows in `out`, so the O projection's GEMM
+    // reads them with planes_ready. Rows past `tokens` are not written (each
+    // GEMM output row depends on its own input row only, and rows past the
+    // token count are never stored). Only where
+    // prompt_attention_writes_planes holds.
+    uint16_t *planes;
+    uint32_t padded;
 };
 hipError_t launch_prompt_attention(hipStream_t, const PromptAttention &);
+bool prompt_attention_writes_planes(uint32_t dim, uint32_t qh, uint32_t kh, uint32_t window);
 // Floats of split scratch launch_prompt_attention uses for this shape (0: none).
 uint64_t prompt_attention_scratch(uint32_t prefix, uint32_t tokens, uint32_t qh, uint32_t kh,
                                   uint32_t dim, uint32_t window);

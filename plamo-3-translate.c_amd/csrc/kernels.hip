@@ -2044,6 +2044,19 @@ __device__ __forceinline__ void write_planes4(uint16_t *planes, uint32_t padded,
     *(u32x2 *)(planes + at + pl) = u32x2{pack_hi16(md[0], md[1]), pack_hi16(md[2], md[3])};
     *(u32x2 *)(planes + at + 2 * pl) = u32x2{pack_hi16(lo[0], lo[1]), pack_hi16(lo[2], lo[3])};
 }
+// One column's value: the same three terms as write_planes4.
+__device__ __forceinline__ void write_planes1(uint16_t *planes, uint32_t padded, uint32_t row,
+                                              uint32_t c, float v) {
+    const uint32_t h = __float_as_uint(v) & 0xffff0000u;
+    const float r = v - __uint_as_float(h);
+    const uint32_t md = __float_as_uint(r) & 0xffff0000u;
+    const uint32_t lo = __float_as_uint(r - __uint_as_float(md));
+    const uint64_t at = ((uint64_t)(c / kSplitBK) * 3 * padded + row) * kSplitBK + c % kSplitBK;
+    const uint64_t pl = (uint64_t)padded * kSplitBK;
+    planes[at] = (uint16_t)(h >> 16);
+    planes[at + pl] = (uint16_t)(md >> 16);
+    planes[at + 2 * pl] = (uint16_t)(lo >> 16);
+}
 
 // norm_rows_kernel with the row held in registers, 16-byte accesses (width a
 // multiple of 4, at most 8192): every load goes out before the sum, where the
@@ -3334,18 +3347,18 @@ __global__ __launch_bounds__(kThreads) void prompt_attention_kernel(PromptAttent
     }
 }
 
-// One block per (token, head): rescales each split's record to the common
-// maximum and normalizes by the combined sum. Splits with no visible key
-// carry a -inf maximum and contribute nothing.
 // One block per (token, head). The splits' maxima and sums are loaded at once
 // (one lane per split) and their factors exp(m_z - m) staged in LDS; then the
 // sum of weights and each output column are accumulated over the splits in
 // split order, skipping splits that saw no key (maximum -inf), as a plain
-// sequential loop over the records would.
+// sequential loop over the records would. With `planes`, each output value
+// is written as its three BF16 terms for the O projection's GEMM instead.
 constexpr uint32_t kMergeSplits = 64;
 __global__ __launch_bounds__(128) void attention_merge_kernel(const float *partial,
                                                               uint32_t splits, uint64_t stride,
-                                                              uint32_t dim, float *out) {
+                                                              uint32_t dim, float *out,
+                                                              uint32_t qh, uint16_t *planes,
+                                                              uint32_t padded) {
     __shared__ float fz[kMergeSplits], lz[kMergeSplits];
     __shared__ uint32_t live[kMergeSplits];
     __shared__ float total;
@@ -3383,7 +3396,11 @@ __global__ __launch_bounds__(128) void attention_merge_kernel(const float *parti
         }
         for (; z < splits; ++z)
             if (live[z]) acc += p[z * stride + d] * fz[z];
-        out[(uint64_t)blockIdx.x * dim + d] = acc / l;
+        const float o = acc / l;
+        if (planes)
+            write_planes1(planes, padded, blockIdx.x / qh, blockIdx.x % qh * dim + d, o);
+        else
+            out[(uint64_t)blockIdx.x * dim + d] = o;
     }
 }
 
@@ -3553,7 +3570,7 @@ __global__ __launch_bounds__(64 * G) void prompt_attention_mfma_kernel(PromptAtt
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
         const uint32_t row = 4 * grp + v;
-        if (row >= nq) continue;
+        if (row >= nq) continue;  // uniform over each 16-lane row of the D layout
         const uint32_t t = t0 + row;
         if (split_rows) {
             // Record [split][token][head]: unnormalized output, running max, sum.
@@ -3567,7 +3584,20 @@ __global__ __launch_bounds__(64 * G) void prompt_attention_mfma_kernel(PromptAtt
         } else {
             float *out = a.out + (uint64_t)t * a.qh * DIM + (uint64_t)h * DIM;
 #pragma unroll
-            for (int n = 0; n < NT; ++n) out[16 * n + col] = o[n][v] / l_run[v];
+            for (int n = 0; n < NT; ++n) {
+                const float y = o[n][v] / l_run[v];
+                if (!a.planes) {
+                    out[16 * n + col] = y;
+                } else {
+                    // Lanes 4j .. 4j + 3 hold four adjacent columns: the
+                    // first writes them as one group of planes.
+                    const float y1 = __shfl_down(y, 1, 4), y2 = __shfl_down(y, 2, 4),
+                                y3 = __shfl_down(y, 3, 4);
+                    if (col % 4 == 0)
+                        write_planes4(a.planes, a.padded, t, h * DIM + 16 * n + col,
+                                      f32x4{y, y1, y2, y3});
+                }
+            }
         }
     }
 }
@@ -3628,8 +3658,17 @@ uint64_t prompt_attention_scratch(uint32_t prefix, uint32_t tokens, uint32_t qh,
     return splits > 1 ? (uint64_t)splits * tokens * qh * (dim + 2) : 0;
 }
 
+bool prompt_attention_writes_planes(uint32_t dim, uint32_t qh, uint32_t kh, uint32_t window) {
+    return prompt_mfma_supported(dim, qh, kh, window);
+}
+
 hipError_t launch_prompt_attention(hipStream_t stream, const PromptAttention &a) {
     if (!a.tokens) return hipSuccess;
+    // Planes come from the matrix-core form only; the scalar form refuses
+    // them rather than leave them unwritten.
+    if (a.planes && (!prompt_mfma_supported(a.dim, a.qh, a.kh, a.window) || a.padded < a.tokens ||
+                     (a.qh * a.dim) % (2 * kSplitBK)))
+        return hipErrorInvalidValue;
     uint32_t rows = 0, splits = 1;
     hipError_t e;
     if (prompt_mfma_supported(a.dim, a.qh, a.kh, a.window)) {
@@ -3646,7 +3685,8 @@ hipError_t launch_prompt_attention(hipStream_t stream, const PromptAttention &a)
     if (e != hipSuccess) return e;
     if (splits > 1)
         attention_merge_kernel<<<a.tokens * a.qh, 128, 0, stream>>>(
-            a.partial, splits, (uint64_t)a.tokens * a.qh * (a.dim + 2), a.dim, a.out);
+            a.partial, splits, (uint64_t)a.tokens * a.qh * (a.dim + 2), a.dim, a.out, a.qh,
+            a.planes, a.padded);
     return hipGetLastError();
 }
 
