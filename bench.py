@@ -692,13 +692,16 @@ def main() -> int:
         f"{step_bytes / ms_step / 1e6:.0f} GB/s of weights")
     assert info1.errors == 0 and info1.cpu_fallbacks == 0, info1.note.decode()
 
-    # Per-kernel HIP-event timings on the backend stream (layer 0 + head).
+    # Per-kernel HIP-event timings on the backend stream (layer 1, whose QKV
+    # prologue adds the previous layer's MLP branch as every layer past the
+    # first does, and the head).
     kernels = {}
+    timed_layer = 1 if inst.model.count > 1 else 0
     names = {plamo_hip.KERNEL_QKV: "qkv_gemv", plamo_hip.KERNEL_O: "o_gemv",
              plamo_hip.KERNEL_GATE_UP: "gate_up_swiglu_gemv", plamo_hip.KERNEL_DOWN: "down_gemv",
              plamo_hip.KERNEL_HEAD: "head_gemv", plamo_hip.KERNEL_ATTENTION: "decode_attention"}
     for which, name in names.items():
-        ms, nbytes = be.time_kernel(inst, 0, which, args.kernel_reps)
+        ms, nbytes = be.time_kernel(inst, timed_layer, which, args.kernel_reps)
         kernels[name] = {"us": round(ms * 1e3, 2), "bytes": int(nbytes),
                          "GBps": round(nbytes / ms / 1e6, 1)}
         log(f"kernel {name}: {ms * 1e3:.2f} us, {nbytes / ms / 1e6:.0f} GB/s")

@@ -2081,6 +2081,15 @@ extern "C" int plamo_hip_time_kernel(struct plamo_metal *m, struct model *model,
             p.src = m->state_a;
             p.w = d.norms;
             p.offset = 1.0f;
+            if (layer) {
+                // After the first layer the prologue also adds the previous
+                // layer's MLP branch (the decode step's state buffers are
+                // rewritten from the embedding at every step).
+                p.branch = m->down_out;
+                p.rw = m->layers[layer - 1].norms + 3 * h;
+                p.roffset = kMlpOffset;
+                p.state_out = m->state_b;
+            }
             return launch_gemv(s, d.qkv, (uint64_t)(d.qh + 2 * d.kh) * d.dim, h, p, m->qkv, 0,
                                blocks);
         case PLAMO_HIP_O:

@@ -3347,43 +3347,38 @@ __global__ __launch_bounds__(kThreads) void prompt_attention_kernel(PromptAttent
     }
 }
 
-// One block per (token, head). The splits' maxima and sums are loaded at once
-// (one lane per split) and their factors exp(m_z - m) staged in LDS; then the
+// One wave per (token, head), four per block. Lane z loads split z's maximum
+// and sum, and the factors exp(m_z - m) go to the wave's LDS slots; then the
 // sum of weights and each output column are accumulated over the splits in
 // split order, skipping splits that saw no key (maximum -inf), as a plain
 // sequential loop over the records would. With `planes`, each output value
 // is written as its three BF16 terms for the O projection's GEMM instead.
 constexpr uint32_t kMergeSplits = 64;
-__global__ __launch_bounds__(128) void attention_merge_kernel(const float *partial,
+__global__ __launch_bounds__(256) void attention_merge_kernel(const float *partial,
                                                               uint32_t splits, uint64_t stride,
                                                               uint32_t dim, float *out,
-                                                              uint32_t qh, uint16_t *planes,
-                                                              uint32_t padded) {
-    __shared__ float fz[kMergeSplits], lz[kMergeSplits];
-    __shared__ uint32_t live[kMergeSplits];
-    __shared__ float total;
-    const float *p = partial + (uint64_t)blockIdx.x * (dim + 2);
-    const uint32_t lane = threadIdx.x;
-    if (lane < 64) {
-        const bool in = lane < splits;
-        const float mz = in ? p[lane * stride + dim] : -__builtin_inff();
-        const float sz = in ? p[lane * stride + dim + 1] : 0.0f;
-        const float m = wave_max(mz);
-        const bool on = mz != -__builtin_inff();
-        fz[lane] = on ? plamo_exp(mz - m) : 0.0f;
-        lz[lane] = sz;
-        live[lane] = on;
-    }
-    __syncthreads();
-    if (lane == 0) {
-        float l = 0.0f;
-        for (uint32_t z = 0; z < splits; ++z)
-            if (live[z]) l += lz[z] * fz[z];
-        total = l;
-    }
-    __syncthreads();
-    const float l = total;
-    for (uint32_t d = lane; d < dim; d += 128) {
+                                                              uint32_t qh, uint32_t pairs,
+                                                              uint16_t *planes, uint32_t padded) {
+    __shared__ float fz_s[4][kMergeSplits], lz_s[4][kMergeSplits];
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t pair = blockIdx.x * 4 + wave;  // token * qh + head
+    if (pair >= pairs) return;  // per wave; the kernel has no block barrier
+    float *fz = fz_s[wave], *lz = lz_s[wave];
+    const float *p = partial + (uint64_t)pair * (dim + 2);
+    const bool in = lane < splits;
+    const float mz = in ? p[lane * stride + dim] : -__builtin_inff();
+    const float sz = in ? p[lane * stride + dim + 1] : 0.0f;
+    const float m = wave_max(mz);
+    const bool on = mz != -__builtin_inff();
+    const uint64_t live = __ballot(on);
+    fz[lane] = on ? plamo_exp(mz - m) : 0.0f;
+    lz[lane] = sz;
+    // The wave's own LDS writes are seen by its later reads (in order).
+    __builtin_amdgcn_wave_barrier();
+    float l = 0.0f;
+    for (uint32_t z = 0; z < splits; ++z)
+        if (live >> z & 1) l += lz[z] * fz[z];
+    for (uint32_t d = lane; d < dim; d += 64) {
         float acc = 0.0f;
         uint32_t z = 0;
         for (; z + 8 <= splits; z += 8) {
@@ -3392,15 +3387,15 @@ __global__ __launch_bounds__(128) void attention_merge_kernel(const float *parti
             for (int j = 0; j < 8; ++j) v[j] = p[(z + j) * stride + d];
 #pragma unroll
             for (int j = 0; j < 8; ++j)
-                if (live[z + j]) acc += v[j] * fz[z + j];
+                if (live >> (z + j) & 1) acc += v[j] * fz[z + j];
         }
         for (; z < splits; ++z)
-            if (live[z]) acc += p[z * stride + d] * fz[z];
+            if (live >> z & 1) acc += p[z * stride + d] * fz[z];
         const float o = acc / l;
         if (planes)
-            write_planes1(planes, padded, blockIdx.x / qh, blockIdx.x % qh * dim + d, o);
+            write_planes1(planes, padded, pair / qh, pair % qh * dim + d, o);
         else
-            out[(uint64_t)blockIdx.x * dim + d] = o;
+            out[(uint64_t)pair * dim + d] = o;
     }
 }
 
@@ -3608,15 +3603,18 @@ static bool prompt_mfma_supported(uint32_t dim, uint32_t qh, uint32_t kh, uint32
     return g == 1 || g == 2 || g == 4 || g == 6 || g == 8 || g == 16;
 }
 
-// Key splits of the matrix-core form: only when its blocks (one per KV head
-// and 16 tokens) leave the GPU mostly idle.
+// Key splits of the matrix-core form, toward about 512 blocks, while its
+// blocks (one per KV head and 16 tokens) number fewer: a causal prompt's
+// last query tiles see every key, and without splits their blocks alone set
+// the launch's length (C4, 443 tokens after a 12-token prefix: 224 blocks,
+// 75-80 us per layer; three splits 45.8 us plus a 12 us merge).
 static uint32_t prompt_mfma_splits(uint32_t prefix, uint32_t tokens, uint32_t qh, uint32_t kh,
                                    uint32_t dim, uint32_t *split_rows) {
     const uint32_t tiles = (tokens + kMQ - 1) / kMQ, keys = prefix + tokens;
     const uint32_t blocks = kh * tiles;
     *split_rows = 0;
-    if (blocks >= 128 || keys <= 2 * kMK) return 1;
-    uint32_t splits = (256 + blocks - 1) / blocks;
+    if (blocks >= 512 || keys <= 2 * kMK) return 1;
+    uint32_t splits = (512 + blocks - 1) / blocks;
     splits = min(splits, min(64u, (keys + kMK - 1) / kMK));
     while (splits > 1 && (uint64_t)splits * tokens * qh * (dim + 2) > kAttentionScratchFloats)
         --splits;
@@ -3684,9 +3682,9 @@ hipError_t launch_prompt_attention(hipStream_t stream, const PromptAttention &a)
     }
     if (e != hipSuccess) return e;
     if (splits > 1)
-        attention_merge_kernel<<<a.tokens * a.qh, 128, 0, stream>>>(
+        attention_merge_kernel<<<(a.tokens * a.qh + 3) / 4, 256, 0, stream>>>(
             a.partial, splits, (uint64_t)a.tokens * a.qh * (a.dim + 2), a.dim, a.out, a.qh,
-            a.planes, a.padded);
+            a.tokens * a.qh, a.planes, a.padded);
     return hipGetLastError();
 }
 
