@@ -1400,8 +1400,10 @@ int run_prompt(plamo_metal *m, struct model *model, const uint32_t *ids, uint64_
     std::vector<char> stale;
     if (!sync_from_host(m, model, stale, !verify)) return -1;
     if (!ensure_prompt(m, model, T) || !ensure_window_scratch(m, model)) return -1;
-    const GemmWorkspace *ws =
-        gemm_workspace(m, T, std::max({h, m->max_attention, m->max_inter}));
+    // Planes room for the widest projection input, and for the gate/up
+    // GEMM's input and activation planes side by side.
+    const GemmWorkspace *ws = gemm_workspace(
+        m, T, std::max({h, m->max_attention, m->max_inter, gemm_swiglu_cols(h, m->max_inter)}));
     if (!ws) return -1;
     if (verify && !m->v_state && !alloc_verify(m, L, h, V)) return -1;
     std::vector<char> overflow(L, 0);
@@ -1616,10 +1618,17 @@ int run_prompt(plamo_metal *m, struct model *model, const uint32_t *ids, uint64_
             // The activation goes to down's GEMM as BF16 planes only, when
             // that GEMM takes the matrix-core route.
             const uint32_t act_planes = gemm_planes_rows(rows, d.inter, ws);
+            uint16_t *act_at = nullptr;
             HIP_FAIL(m, launch_gemm_swiglu(s, norm, h, d.gu, d.inter, h, rows, act, gu, ws,
-                                          gu_planes, act_planes));
-            HIP_FAIL(m, launch_gemm(s, act, d.inter, d.down, h, d.inter, rows, branch, h, ws,
-                                    act_planes != 0));
+                                          gu_planes, act_planes, &act_at));
+            // Down reads the activation planes where the gate/up launch put them.
+            GemmWorkspace down_ws = *ws;
+            if (act_planes) {
+                down_ws.planes = act_at;
+                down_ws.plane_elems = ws->plane_elems - (uint64_t)(act_at - ws->planes);
+            }
+            HIP_FAIL(m, launch_gemm(s, act, d.inter, d.down, h, d.inter, rows, branch, h,
+                                    &down_ws, act_planes != 0));
             if (fuse_rows && i + 1 < L) {
                 const uint32_t tp = gemm_planes_rows(rows, h, ws);
                 HIP_FAIL(m, launch_residual_norm_rows(s, st, branch, mpost, kMlpOffset,
@@ -1634,7 +1643,7 @@ int run_prompt(plamo_metal *m, struct model *model, const uint32_t *ids, uint64_
             } else {
                 HIP_FAIL(m, launch_residual_rows(s, st, branch, mpost, kMlpOffset, h, rows));
             }
-            n += 6;
+            n += act_planes && act_at != ws->planes ? 5 : 6;  // the SwiGLU in gate/up's epilogue
         }
     }
     if (verify) {

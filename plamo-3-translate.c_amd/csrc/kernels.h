@@ -82,6 +82,13 @@ struct GemmSplit {
     uint32_t *counters;
     uint16_t *planes;
     uint32_t xcd_group;  // nonzero: the M tiles of a weight tile share an XCD (see the kernel)
+    // Nonzero (the intermediate size I): the rows are a gate/up pair [2I]
+    // and each tile takes gate and up rows of the same intermediate columns;
+    // the epilogue writes silu(gate) * up as the BF16 planes `act` (rows
+    // padded to act_tp) instead of y.
+    uint32_t swiglu;
+    uint16_t *act;
+    uint32_t act_tp;
 };
 constexpr uint64_t kGemmPartialFloats = 16ull << 20;  // 64 MiB
 constexpr uint32_t kGemmCounters = 8192;
@@ -130,12 +137,22 @@ hipError_t launch_swiglu_rows(hipStream_t, const float *gate_up, float *out,
 // intermediate + i of w): the token GEMV writes act directly; other shapes
 // go through launch_gemm into gate_up ([tokens][2 * intermediate]) and
 // launch_swiglu_rows. act_planes (gemm_planes_rows(tokens, intermediate, ws),
-// nonzero) writes the activation only as the workspace planes, for a
-// launch_gemm of act with planes_ready; shapes without that route fail.
+// nonzero) writes the activation only as BF16 planes, for a launch_gemm of
+// act with planes_ready over `ws` with its planes at *act_at: when the
+// workspace holds the input's planes and the activation's side by side, the
+// gate/up GEMM forms them in its epilogue (*act_at past the input's);
+// otherwise a separate SwiGLU launch writes them at ws->planes. Shapes
+// without either route fail.
 hipError_t launch_gemm_swiglu(hipStream_t, const float *x, uint64_t x_stride, const uint16_t *w,
                               uint64_t intermediate, uint64_t cols, uint64_t tokens, float *act,
                               float *gate_up, const GemmWorkspace *ws, bool planes_ready = false,
-                              uint32_t act_planes = 0);
+                              uint32_t act_planes = 0, uint16_t **act_at = nullptr);
+// The workspace columns a launch_gemm_swiglu over `cols` input columns needs
+// for its epilogue to write the activation planes (input and activation
+// planes side by side).
+inline uint64_t gemm_swiglu_cols(uint64_t cols, uint64_t intermediate) {
+    return cols + intermediate;
+}
 
 // Q/K head RMSNorm + RoPE + cache append for `tokens` rows of one layer.
 struct QkvPost {

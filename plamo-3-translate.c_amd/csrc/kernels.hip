@@ -1074,6 +1074,38 @@ __device__ __forceinline__ uint32_t pack_hi16(uint32_t a, uint32_t b) {
 __device__ __forceinline__ uint32_t swizzle(uint32_t r, uint32_t q) {
     return q ^ ((r ^ (r >> 2)) & 3);
 }
+// Columns c .. c + 3 of row `row` into the BF16 planes of launch_gemm's
+// matrix-core path (the layout split_planes_kernel writes: [c / 32][plane]
+// [padded row][c % 32], the exact three-term split).
+__device__ __forceinline__ void write_planes4(uint16_t *planes, uint32_t padded, uint32_t row,
+                                              uint32_t c, f32x4 v) {
+    uint32_t h[4], md[4], lo[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        h[e] = __float_as_uint(v[e]) & 0xffff0000u;
+        const float r = v[e] - __uint_as_float(h[e]);
+        md[e] = __float_as_uint(r) & 0xffff0000u;
+        lo[e] = __float_as_uint(r - __uint_as_float(md[e]));
+    }
+    const uint64_t at = ((uint64_t)(c / kSplitBK) * 3 * padded + row) * kSplitBK + c % kSplitBK;
+    const uint64_t pl = (uint64_t)padded * kSplitBK;
+    *(u32x2 *)(planes + at) = u32x2{pack_hi16(h[0], h[1]), pack_hi16(h[2], h[3])};
+    *(u32x2 *)(planes + at + pl) = u32x2{pack_hi16(md[0], md[1]), pack_hi16(md[2], md[3])};
+    *(u32x2 *)(planes + at + 2 * pl) = u32x2{pack_hi16(lo[0], lo[1]), pack_hi16(lo[2], lo[3])};
+}
+// One column's value: the same three terms as write_planes4.
+__device__ __forceinline__ void write_planes1(uint16_t *planes, uint32_t padded, uint32_t row,
+                                              uint32_t c, float v) {
+    const uint32_t h = __float_as_uint(v) & 0xffff0000u;
+    const float r = v - __uint_as_float(h);
+    const uint32_t md = __float_as_uint(r) & 0xffff0000u;
+    const uint32_t lo = __float_as_uint(r - __uint_as_float(md));
+    const uint64_t at = ((uint64_t)(c / kSplitBK) * 3 * padded + row) * kSplitBK + c % kSplitBK;
+    const uint64_t pl = (uint64_t)padded * kSplitBK;
+    planes[at] = (uint16_t)(h >> 16);
+    planes[at + pl] = (uint16_t)(md >> 16);
+    planes[at + 2 * pl] = (uint16_t)(lo >> 16);
+}
 
 __global__ __launch_bounds__(256) void split_planes_kernel(const float *x, uint64_t ldx,
                                                            uint32_t rows, uint32_t padded,
@@ -1148,12 +1180,22 @@ __global__ __launch_bounds__(64 * GM * GN, (WN > 2 || GM * GN > 4) ? 1 : 2) void
         asrc[i] = g.planes + ((uint64_t)p * g.tp + m0 + r) * kSplitBK + 8 * q;
         adst[i] = R * 4 + swizzle(R, q);
     }
+    // With swiglu, tile row r of wave column wn and 32-row group j takes the
+    // gate (j even) or up (j odd) row of intermediate column
+    // bn BN/2 + wn 16 WN + (j / 2) 32 + r % 32: a lane's accumulators j and
+    // j + 1 then hold the gate and up sums of one column.
     const uint16_t *wsrc[WPT];
     uint32_t wdst[WPT];
 #pragma unroll
     for (int i = 0; i < WPT; ++i) {
         const uint32_t G = threadIdx.x + NT * i, r = G / 4, q = G % 4;
-        wsrc[i] = g.w + (uint64_t)min(n0 + r, g.n - 1) * g.k + 8 * q;
+        uint32_t row = min(n0 + r, g.n - 1);
+        if (g.swiglu) {
+            const uint32_t j = r / 32 % WN;
+            const uint32_t col = bn * (BN / 2) + r / (32 * WN) * (16 * WN) + j / 2 * 32 + r % 32;
+            row = (j & 1) ? g.swiglu + col : col;
+        }
+        wsrc[i] = g.w + (uint64_t)row * g.k + 8 * q;
         wdst[i] = AG + r * 4 + swizzle(r, q);
     }
     u32x4 av[PD][APT], wv[PD][WPT];
@@ -1280,6 +1322,25 @@ __global__ __launch_bounds__(64 * GM * GN, (WN > 2 || GM * GN > 4) ? 1 : 2) void
             for (int j = 0; j < WN; ++j)
 #pragma unroll
                 for (int v = 0; v < 16; ++v) acc[i][j][v] = sum[i][j][v];
+    }
+    if (g.swiglu) {
+        // silu(gate) * up as in swiglu_planes_kernel (tests/activation_reference.s:99-126),
+        // written as the activation's BF16 planes; padding rows are not written.
+#pragma unroll
+        for (int i = 0; i < WM; ++i)
+#pragma unroll
+            for (int j = 0; j < WN; j += 2) {
+                const uint32_t col = bn * (BN / 2) + wn * 16 * WN + j / 2 * 32 + (lane & 31);
+#pragma unroll
+                for (int v = 0; v < 16; ++v) {
+                    const uint32_t row =
+                        m0 + wm * 32 * WM + 32 * i + 8 * (v / 4) + 4 * (lane >> 5) + v % 4;
+                    const float gate = acc[i][j][v], up = acc[i][j + 1][v];
+                    const float d = plamo_exp(-gate) + 1.0f;
+                    if (row < g.t) write_planes1(g.act, g.act_tp, row, col, (gate / d) * up);
+                }
+            }
+        return;
     }
 #pragma unroll
     for (int i = 0; i < WM; ++i)
@@ -1928,6 +1989,34 @@ uint32_t gemm_planes_rows(uint64_t tokens, uint64_t cols, const GemmWorkspace *w
                : 0;
 }
 
+// The matrix-core GEMM's tiling for g.n rows, g.t tokens (every tiling has
+// an even number of 32-row groups per wave, as a swiglu launch needs).
+static hipError_t gemm_split_route(hipStream_t stream, const GemmSplit &g, const GemmWorkspace &ws,
+                                   bool planes_ready) {
+    const uint64_t rows = g.n, tokens = g.t;
+    // Wide tiles (128 tokens x 256 rows per block, as 8 waves of 64 x 64:
+    // two waves per SIMD) when there are enough of them: fewer LDS bytes
+    // per MFMA and half the re-reads of X.
+    const bool wide = (rows + 255) / 256 * ((tokens + 127) / 128) >= 64;
+    // Up to 128 tokens, 64-token tiles: a 65-128-token prompt gets two M
+    // tiles (the xcd_group order keeps each weight tile in one XCD's L2),
+    // fewer K splits and twice the blocks with half the work each (C4
+    // TTFT@128 prefill 10.7 -> 9.7 ms; with three K stages of prefetch
+    // 9.9). 443 tokens stay on 128-token tiles (64: 27.6 -> 31.8 ms).
+    if (tokens <= 128)
+        return wide ? gemm_split_variant<1, 4, 2, 2, 4>(stream, g, ws, planes_ready)
+                    : gemm_split_variant<1, 2, 2, 2, 4>(stream, g, ws, planes_ready);
+    // Four K stages in registers ahead of the LDS stage (3: TTFT@128
+    // 11.43 ms, 4: 11.19, 5 and 6 slower).
+    return wide ? gemm_split_variant<2, 2, 2, 4, 4>(stream, g, ws, planes_ready)
+                : gemm_split_variant<2, 2, 2, 2, 4>(stream, g, ws, planes_ready);
+}
+// Rows of one tile of the route above (the swiglu pairing needs the
+// intermediate size to be whole half tiles).
+static uint32_t gemm_split_tile_rows(uint64_t rows, uint64_t tokens) {
+    return (rows + 255) / 256 * ((tokens + 127) / 128) >= 64 ? 256 : 128;
+}
+
 hipError_t launch_gemm(hipStream_t stream, const float *x, uint64_t x_stride, const uint16_t *w,
                        uint64_t rows, uint64_t cols, uint64_t tokens, float *y,
                        uint64_t y_stride, const GemmWorkspace *ws, bool planes_ready) {
@@ -1966,22 +2055,7 @@ hipError_t launch_gemm(hipStream_t stream, const float *x, uint64_t x_stride, co
         g.t = (uint32_t)tokens;
         g.y = y;
         g.ldy = y_stride;
-        // Wide tiles (128 tokens x 256 rows per block, as 8 waves of 64 x 64:
-        // two waves per SIMD) when there are enough of them: fewer LDS bytes
-        // per MFMA and half the re-reads of X.
-        const bool wide = (rows + 255) / 256 * ((tokens + 127) / 128) >= 64;
-        // Up to 128 tokens, 64-token tiles: a 65-128-token prompt gets two M
-        // tiles (the xcd_group order keeps each weight tile in one XCD's L2),
-        // fewer K splits and twice the blocks with half the work each (C4
-        // TTFT@128 prefill 10.7 -> 9.7 ms; with three K stages of prefetch
-        // 9.9). 443 tokens stay on 128-token tiles (64: 27.6 -> 31.8 ms).
-        if (tokens <= 128)
-            return wide ? gemm_split_variant<1, 4, 2, 2, 4>(stream, g, *ws, planes_ready)
-                        : gemm_split_variant<1, 2, 2, 2, 4>(stream, g, *ws, planes_ready);
-        // Four K stages in registers ahead of the LDS stage (3: TTFT@128
-        // 11.43 ms, 4: 11.19, 5 and 6 slower).
-        return wide ? gemm_split_variant<2, 2, 2, 4, 4>(stream, g, *ws, planes_ready)
-                    : gemm_split_variant<2, 2, 2, 2, 4>(stream, g, *ws, planes_ready);
+        return gemm_split_route(stream, g, *ws, planes_ready);
     }
     if (planes_ready) return hipErrorInvalidValue;
     if (tokens <= 16) return gemm_variant<16, 64>(stream, x, x_stride, w, rows, cols, tokens, y, y_stride);
@@ -1991,11 +2065,38 @@ hipError_t launch_gemm(hipStream_t stream, const float *x, uint64_t x_stride, co
 hipError_t launch_gemm_swiglu(hipStream_t stream, const float *x, uint64_t x_stride,
                               const uint16_t *w, uint64_t intermediate, uint64_t cols,
                               uint64_t tokens, float *act, float *gate_up,
-                              const GemmWorkspace *ws, bool planes_ready, uint32_t act_planes) {
+                              const GemmWorkspace *ws, bool planes_ready, uint32_t act_planes,
+                              uint16_t **act_at) {
+    if (act_at) *act_at = ws ? ws->planes : nullptr;
     if (!tokens || !intermediate) return hipSuccess;
     // Checked before anything is launched: a failure leaves the stream as it was.
-    if (act_planes && (!ws || !ws->planes || 3ull * act_planes * intermediate > ws->plane_elems))
+    if (act_planes && (!ws || !ws->planes || 3ull * act_planes * intermediate > ws->plane_elems ||
+                       act_planes < tokens || intermediate % (2 * kSplitBK) ||
+                       intermediate >= (1u << 30) || ((uintptr_t)gate_up & 15)))
         return hipErrorInvalidValue;
+    // The gate/up GEMM writes the activation planes from its epilogue, past
+    // the input's planes (which its running blocks still read), when the
+    // workspace holds both: one launch less and no FP32 gate/up rows.
+    if (act_planes && act_at && tokens > kSkinnyTokens && tokens < (1u << 31) &&
+        2 * intermediate < (1u << 31) && gemm_split_supported(x, x_stride, w, cols) &&
+        intermediate % (gemm_split_tile_rows(2 * intermediate, tokens) / 2) == 0 &&
+        gemm_planes_rows(tokens, cols, ws) == act_planes) {
+        const uint64_t in_elems = 3ull * act_planes * cols;
+        if (in_elems + 3ull * act_planes * intermediate <= ws->plane_elems) {
+            GemmSplit g{};
+            g.x = x;
+            g.ldx = x_stride;
+            g.w = w;
+            g.n = (uint32_t)(2 * intermediate);
+            g.k = (uint32_t)cols;
+            g.t = (uint32_t)tokens;
+            g.swiglu = (uint32_t)intermediate;
+            g.act = ws->planes + in_elems;
+            g.act_tp = act_planes;
+            *act_at = g.act;
+            return gemm_split_route(stream, g, *ws, planes_ready);
+        }
+    }
     // The token GEMV reads x and writes act as FP32 only: it takes neither
     // input planes in place of x nor planes for the output.
     if (!planes_ready && !act_planes) {
@@ -2025,38 +2126,6 @@ __global__ __launch_bounds__(kThreads) void norm_rows_kernel(const float *x, uin
     }
 }
 
-// Columns c .. c + 3 of row `row` into the BF16 planes of launch_gemm's
-// matrix-core path (the layout split_planes_kernel writes: [c / 32][plane]
-// [padded row][c % 32], the exact three-term split).
-__device__ __forceinline__ void write_planes4(uint16_t *planes, uint32_t padded, uint32_t row,
-                                              uint32_t c, f32x4 v) {
-    uint32_t h[4], md[4], lo[4];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        h[e] = __float_as_uint(v[e]) & 0xffff0000u;
-        const float r = v[e] - __uint_as_float(h[e]);
-        md[e] = __float_as_uint(r) & 0xffff0000u;
-        lo[e] = __float_as_uint(r - __uint_as_float(md[e]));
-    }
-    const uint64_t at = ((uint64_t)(c / kSplitBK) * 3 * padded + row) * kSplitBK + c % kSplitBK;
-    const uint64_t pl = (uint64_t)padded * kSplitBK;
-    *(u32x2 *)(planes + at) = u32x2{pack_hi16(h[0], h[1]), pack_hi16(h[2], h[3])};
-    *(u32x2 *)(planes + at + pl) = u32x2{pack_hi16(md[0], md[1]), pack_hi16(md[2], md[3])};
-    *(u32x2 *)(planes + at + 2 * pl) = u32x2{pack_hi16(lo[0], lo[1]), pack_hi16(lo[2], lo[3])};
-}
-// One column's value: the same three terms as write_planes4.
-__device__ __forceinline__ void write_planes1(uint16_t *planes, uint32_t padded, uint32_t row,
-                                              uint32_t c, float v) {
-    const uint32_t h = __float_as_uint(v) & 0xffff0000u;
-    const float r = v - __uint_as_float(h);
-    const uint32_t md = __float_as_uint(r) & 0xffff0000u;
-    const uint32_t lo = __float_as_uint(r - __uint_as_float(md));
-    const uint64_t at = ((uint64_t)(c / kSplitBK) * 3 * padded + row) * kSplitBK + c % kSplitBK;
-    const uint64_t pl = (uint64_t)padded * kSplitBK;
-    planes[at] = (uint16_t)(h >> 16);
-    planes[at + pl] = (uint16_t)(md >> 16);
-    planes[at + 2 * pl] = (uint16_t)(lo >> 16);
-}
 
 // norm_rows_kernel with the row held in registers, 16-byte accesses (width a
 // multiple of 4, at most 8192): every load goes out before the sum, where the
