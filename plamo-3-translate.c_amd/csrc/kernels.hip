@@ -1066,6 +1066,7 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int kSplitBK = 32;  // K per stage: four 16-byte granules of BF16 per row
+constexpr uint32_t kSplitBM = 64;  // tokens per block of every routed tiling (two waves of 32)
 
 __device__ __forceinline__ uint32_t pack_hi16(uint32_t a, uint32_t b) {
     return (b & 0xffff0000u) | (a >> 16);
@@ -1208,8 +1209,7 @@ __global__ __launch_bounds__(64 * GM * GN, (WN > 2 || GM * GN > 4) ? 1 : 2) void
             av[slot][i] = *(const u32x4 *)(asrc[i] + (uint64_t)ks * stage_elems);
 #pragma unroll
         for (int i = 0; i < WPT; ++i)
-            wv[slot][i] =
-                __builtin_nontemporal_load((const u32x4 *)(wsrc[i] + (uint64_t)ks * kSplitBK));
+            wv[slot][i] = *(const u32x4 *)(wsrc[i] + (uint64_t)ks * kSplitBK);
     };
     auto store = [&](int slot, int buf) {
         u32x4 *st = lds + buf * SG;
@@ -1360,6 +1360,7 @@ template <int WM, int WN, int GM = 2, int GN = 2, int PD = 3>
 static hipError_t gemm_split_variant(hipStream_t stream, GemmSplit g, const GemmWorkspace &ws,
                                      bool planes_ready = false) {
     constexpr uint32_t BM = 32 * WM * GM, BN = 32 * WN * GN;
+    static_assert(BM == kSplitBM, "gemm_planes_rows pads the planes to kSplitBM rows");
     const uint32_t nt = (g.n + BN - 1) / BN, mt = (g.t + BM - 1) / BM;
     const uint32_t tiles = nt * mt, stages = g.k / kSplitBK;
     g.tp = mt * BM;
@@ -1983,38 +1984,41 @@ uint32_t gemm_planes_rows(uint64_t tokens, uint64_t cols, const GemmWorkspace *w
     if (tokens <= kSkinnyTokens || tokens >= (1u << 31) || cols % (2 * kSplitBK) ||
         cols > (1u << 30) || !ws || !ws->planes)
         return 0;
-    const uint64_t bm = tokens <= 128 ? 64 : 128, tp = (tokens + bm - 1) / bm * bm;
+    const uint64_t tp = (tokens + kSplitBM - 1) / kSplitBM * kSplitBM;
     return 3 * tp * cols <= ws->plane_elems && gemm_plane_elems(tokens, cols) <= ws->plane_elems
                ? (uint32_t)tp
                : 0;
 }
 
-// The matrix-core GEMM's tiling for g.n rows, g.t tokens (every tiling has
-// an even number of 32-row groups per wave, as a swiglu launch needs).
+// Wide tiles (256 weight rows per block, each wave 32 tokens x 128 rows)
+// except for short prompts' projections with few row tiles and K below 8192,
+// which take 128-row tiles (each wave 32 x 64) and get more blocks. Measured
+// per C4 projection at 69-1024 tokens against 128-token tiles of 8 waves
+// (64 x 64 each): the wide 64-token tiles win from 200 tokens on (443: QKV
+// 125.7 -> 101.4 us, O 76.1 -> 64.4, gate/up 433.6 -> 399.9, down 227.6 ->
+// 213.1), and down at 116 (76.3 -> 75.2, K 16384).
+static bool gemm_split_wide(uint64_t rows, uint64_t cols, uint64_t tokens) {
+    return tokens > 128 || cols >= 8192 || (rows + 255) / 256 >= 64;
+}
+// The matrix-core GEMM's tiling for g.n rows, g.t tokens (both tilings have
+// an even number of 32-row groups per wave, as a swiglu launch needs). Four
+// K stages in registers ahead of the LDS stage (3 and 6 measured slower).
+// The weights are read with ordinary loads: each 64-byte stage of a row is
+// half a 128-byte cache line whose other half the next stage reads, and
+// non-temporal loads, which let the line go, measured slower in place (C4 at
+// 443 tokens: QKV 114.1 -> 97.2 us, O 67.9 -> 60.6, gate/up 381.9 -> 362.5,
+// down 200.0 -> 187.5; at 116: QKV 40.6 -> 36.9, gate/up equal within the
+// spread between boxes).
 static hipError_t gemm_split_route(hipStream_t stream, const GemmSplit &g, const GemmWorkspace &ws,
                                    bool planes_ready) {
-    const uint64_t rows = g.n, tokens = g.t;
-    // Wide tiles (128 tokens x 256 rows per block, as 8 waves of 64 x 64:
-    // two waves per SIMD) when there are enough of them: fewer LDS bytes
-    // per MFMA and half the re-reads of X.
-    const bool wide = (rows + 255) / 256 * ((tokens + 127) / 128) >= 64;
-    // Up to 128 tokens, 64-token tiles: a 65-128-token prompt gets two M
-    // tiles (the xcd_group order keeps each weight tile in one XCD's L2),
-    // fewer K splits and twice the blocks with half the work each (C4
-    // TTFT@128 prefill 10.7 -> 9.7 ms; with three K stages of prefetch
-    // 9.9). 443 tokens stay on 128-token tiles (64: 27.6 -> 31.8 ms).
-    if (tokens <= 128)
-        return wide ? gemm_split_variant<1, 4, 2, 2, 4>(stream, g, ws, planes_ready)
-                    : gemm_split_variant<1, 2, 2, 2, 4>(stream, g, ws, planes_ready);
-    // Four K stages in registers ahead of the LDS stage (3: TTFT@128
-    // 11.43 ms, 4: 11.19, 5 and 6 slower).
-    return wide ? gemm_split_variant<2, 2, 2, 4, 4>(stream, g, ws, planes_ready)
-                : gemm_split_variant<2, 2, 2, 2, 4>(stream, g, ws, planes_ready);
+    return gemm_split_wide(g.n, g.k, g.t)
+               ? gemm_split_variant<1, 4, 2, 2, 4>(stream, g, ws, planes_ready)
+               : gemm_split_variant<1, 2, 2, 2, 4>(stream, g, ws, planes_ready);
 }
 // Rows of one tile of the route above (the swiglu pairing needs the
 // intermediate size to be whole half tiles).
-static uint32_t gemm_split_tile_rows(uint64_t rows, uint64_t tokens) {
-    return (rows + 255) / 256 * ((tokens + 127) / 128) >= 64 ? 256 : 128;
+static uint32_t gemm_split_tile_rows(uint64_t rows, uint64_t cols, uint64_t tokens) {
+    return gemm_split_wide(rows, cols, tokens) ? 256 : 128;
 }
 
 hipError_t launch_gemm(hipStream_t stream, const float *x, uint64_t x_stride, const uint16_t *w,
@@ -2079,7 +2083,7 @@ hipError_t launch_gemm_swiglu(hipStream_t stream, const float *x, uint64_t x_str
     // workspace holds both: one launch less and no FP32 gate/up rows.
     if (act_planes && act_at && tokens > kSkinnyTokens && tokens < (1u << 31) &&
         2 * intermediate < (1u << 31) && gemm_split_supported(x, x_stride, w, cols) &&
-        intermediate % (gemm_split_tile_rows(2 * intermediate, tokens) / 2) == 0 &&
+        intermediate % (gemm_split_tile_rows(2 * intermediate, cols, tokens) / 2) == 0 &&
         gemm_planes_rows(tokens, cols, ws) == act_planes) {
         const uint64_t in_elems = 3ull * act_planes * cols;
         if (in_elems + 3ull * act_planes * intermediate <= ws->plane_elems) {
