@@ -74,7 +74,12 @@ PROMPTS = [1, 2, 3, 4, 7, 8, 9, 17, 31, 32, 33, 116, 128, 129, 255, 256, 257, 44
            4096]
 
 
-@pytest.mark.parametrize("h,inter,dim,capacity", [(7, 11, 6, 4100), (128, 257, 128, 600)])
+# (256, 384): every projection past 16 tokens takes the matrix-core GEMM on
+# BF16 planes written by its producer (the norms, the prompt attention, and
+# the gate/up GEMM's SwiGLU epilogue for down), over one and several 64-token
+# tiles and K splits.
+@pytest.mark.parametrize("h,inter,dim,capacity",
+                         [(7, 11, 6, 4100), (128, 257, 128, 600), (256, 384, 128, 600)])
 def test_prefill_then_decode(h, inter, dim, capacity):
     s = tiny(h=h, inter=inter, dim=dim, capacity=capacity)
     a, b = s.instance(), s.instance()
