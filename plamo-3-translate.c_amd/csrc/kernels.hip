@@ -1054,7 +1054,7 @@ static hipError_t gemm_variant(hipStream_t stream, const float *x, uint64_t x_st
 // padding rows zero), so one stage of a row tile is contiguous.
 // The GEMM block is 4 waves as 2 x 2, each wave WM x WN tiles of 32 x 32, so
 // a block covers BM = 64 WM token rows by BN = 64 WN weight rows; K advances
-// 32 per stage through double-buffered LDS (two blocks per CU for WN = 2), with
+// 32 per stage through three LDS buffers (two blocks per CU for WN = 2), with
 // PD stages in flight in registers. Each block starts its K loop at its
 // own stage (rotating): weight rows are a multiple of 4 KB apart, so blocks in
 // lockstep would all read one memory channel. LDS rows are 64 bytes with their four
@@ -1148,7 +1148,7 @@ __global__ __launch_bounds__(64 * GM * GN, (WN > 2 || GM * GN > 4) ? 1 : 2) void
     constexpr int AG = 3 * BM * 4, WG = BN * 4, SG = AG + WG;  // granules per stage
     constexpr int APT = AG / NT, WPT = WG / NT;                 // granules per thread
     static_assert(AG % NT == 0 && WG % NT == 0, "whole granules per thread");
-    extern __shared__ u32x4 lds[];                               // [2][SG]
+    extern __shared__ u32x4 lds[];                               // [3][SG]
     __shared__ int is_last;
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const uint32_t wm = wave / GN, wn = wave % GN;
@@ -1211,12 +1211,29 @@ __global__ __launch_bounds__(64 * GM * GN, (WN > 2 || GM * GN > 4) ? 1 : 2) void
         for (int i = 0; i < WPT; ++i)
             wv[slot][i] = *(const u32x4 *)(wsrc[i] + (uint64_t)ks * kSplitBK);
     };
-    auto store = [&](int slot, int buf) {
+    auto store = [&](int slot, uint32_t buf) {
         u32x4 *st = lds + buf * SG;
 #pragma unroll
         for (int i = 0; i < APT; ++i) st[adst[i]] = av[slot][i];
 #pragma unroll
         for (int i = 0; i < WPT; ++i) st[wdst[i]] = wv[slot][i];
+    };
+    // Fragments of K step ks (16 columns) of the stage in LDS buffer buf.
+    auto frag = [&](uint32_t buf, int ks, bf16x8 (&a)[3][WM], bf16x8 (&b)[WN]) {
+        const u32x4 *st = lds + buf * SG;
+        const uint32_t q = 2 * ks + (lane >> 5);
+#pragma unroll
+        for (int i = 0; i < WM; ++i)
+#pragma unroll
+            for (int p = 0; p < 3; ++p) {
+                const uint32_t R = p * BM + wm * 32 * WM + 32 * i + (lane & 31);
+                a[p][i] = __builtin_bit_cast(bf16x8, st[R * 4 + swizzle(R, q)]);
+            }
+#pragma unroll
+        for (int j = 0; j < WN; ++j) {
+            const uint32_t r = wn * 32 * WN + 32 * j + (lane & 31);
+            b[j] = __builtin_bit_cast(bf16x8, st[AG + r * 4 + swizzle(r, q)]);
+        }
     };
 
     f32x16 acc[WM][WN];
@@ -1226,57 +1243,78 @@ __global__ __launch_bounds__(64 * GM * GN, (WN > 2 || GM * GN > 4) ? 1 : 2) void
         for (int j = 0; j < WN; ++j)
 #pragma unroll
             for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
-
-    auto compute = [&](int buf) {
-        const u32x4 *st = lds + buf * SG;
+    auto mfma = [&](const bf16x8 (&a)[3][WM], const bf16x8 (&b)[WN]) {
 #pragma unroll
-        for (int ks = 0; ks < kSplitBK / 16; ++ks) {
-            const uint32_t q = 2 * ks + (lane >> 5);
-            bf16x8 a[3][WM], b[WN];
+        for (int p = 0; p < 3; ++p)
 #pragma unroll
-            for (int i = 0; i < WM; ++i) {
+            for (int i = 0; i < WM; ++i)
 #pragma unroll
-                for (int p = 0; p < 3; ++p) {
-                    const uint32_t R = p * BM + wm * 32 * WM + 32 * i + (lane & 31);
-                    a[p][i] = __builtin_bit_cast(bf16x8, st[R * 4 + swizzle(R, q)]);
-                }
-            }
-#pragma unroll
-            for (int j = 0; j < WN; ++j) {
-                const uint32_t r = wn * 32 * WN + 32 * j + (lane & 31);
-                b[j] = __builtin_bit_cast(bf16x8, st[AG + r * 4 + swizzle(r, q)]);
-            }
-#pragma unroll
-            for (int p = 0; p < 3; ++p)
-#pragma unroll
-                for (int i = 0; i < WM; ++i)
-#pragma unroll
-                    for (int j = 0; j < WN; ++j)
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[p][i], b[j],
-                                                                             acc[i][j], 0, 0, 0);
-        }
+                for (int j = 0; j < WN; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[p][i], b[j], acc[i][j],
+                                                                         0, 0, 0);
     };
 
-    // Stage j lives in register slot j % PD and LDS buffer j % 2. Loads are
-    // unconditional (clamped to the last stage) so the compiler keeps exact
-    // wait counts; the step count is padded to a multiple of PD.
+    // Three LDS buffers: stage j + 1 is already in LDS (written during step
+    // j - 1) while step j computes stage j, so step j reads the fragments of
+    // its own second K step and of stage j + 1's first K step under its
+    // MFMAs, writes stage j + 2 into the third buffer, and the next step
+    // starts on its MFMAs right after the one barrier per step. Stage s
+    // lives in register slot s % PD from its load (step s - 2 - PD) to its
+    // LDS write (step s - 2). Loads past the last stage are clamped to it, so
+    // every step issues the same loads and the compiler keeps exact wait
+    // counts; writes past the last stage land in a buffer no step reads.
+    // Every split has at least two stages (K is a multiple of 64).
 #pragma unroll
     for (int sl = 0; sl < PD; ++sl) load(sl, sl);
     store(0, 0);
+    store(1 % PD, 1);
+    load(0, PD);
+    load(1 % PD, PD + 1);
     __syncthreads();
-    int buf = 0;
-    auto step = [&](uint32_t j, int slot) {
-        load(slot, j + PD);
-        if (j < nst) {
-            compute(buf);
-            if (j + 1 < nst) store((slot + 1) % PD, buf ^ 1);
-        }
-        __syncthreads();
-        buf ^= 1;
-    };
-    for (uint32_t j = 0; j < nst; j += PD) {
+    constexpr int NF = 3 * WM + WN, NMF = 3 * WM * WN;  // reads, MFMAs per K step
+    bf16x8 a0[3][WM], b0[WN], a1[3][WM], b1[WN];
+    frag(0, 0, a0, b0);
+    uint32_t cur = 0;  // LDS buffer of stage j
+    for (uint32_t j0 = 0; j0 < nst; j0 += PD) {
 #pragma unroll
-        for (int sl = 0; sl < PD; ++sl) step(j + sl, sl);
+        for (int sl = 0; sl < PD; ++sl) {
+            const uint32_t j = j0 + sl;
+            const int ps = (sl + 2) % PD;  // register slot of stage j + 2
+            const uint32_t nxt = cur == 2 ? 0 : cur + 1, nn = nxt == 2 ? 0 : nxt + 1;
+            if (j < nst) {
+                frag(cur, 1, a1, b1);
+                mfma(a0, b0);
+                store(ps, nn);
+                load(ps, j + 2 + PD);
+                frag(nxt, 0, a0, b0);
+                mfma(a1, b1);
+                // Issue order: per MFMA one second-step read, then one LDS
+                // write with one global load, then one next-stage read; the
+                // matrix cores never wait behind the barrier for LDS (C4
+                // prefill GEMMs 7-12 % faster than reads after the barrier and
+                // writes after the MFMAs).
+#pragma unroll
+                for (int i = 0; i < NF; ++i) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // LDS read
+                }
+#pragma unroll
+                for (int i = 0; i < APT + WPT; ++i) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);  // LDS write
+                    __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // global load
+                }
+#pragma unroll
+                for (int i = 0; i < NF; ++i) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                }
+                if constexpr (2 * NMF > 2 * NF + APT + WPT)
+                    __builtin_amdgcn_sched_group_barrier(0x008, 2 * NMF - 2 * NF - APT - WPT, 0);
+            }
+            __syncthreads();
+            cur = nxt;
+        }
     }
 
     // D layout of v_mfma_f32_32x32x16: value v of lane l is row
@@ -1386,7 +1424,7 @@ static hipError_t gemm_split_variant(hipStream_t stream, GemmSplit g, const Gemm
     if (!planes_ready)
         split_planes_kernel<<<(unsigned)((elems / 8 + 255) / 256), 256, 0, stream>>>(
             g.x, g.ldx, g.t, g.tp, g.k, ws.planes);
-    const size_t lds = 2 * (size_t)(3 * BM * 4 + BN * 4) * sizeof(u32x4);
+    const size_t lds = 3 * (size_t)(3 * BM * 4 + BN * 4) * sizeof(u32x4);
     static bool attr = false;
     if (!attr) {
         hipError_t e = hipFuncSetAttribute((const void *)gemm_split_kernel<WM, WN, GM, GN, PD>,
@@ -2001,8 +2039,9 @@ static bool gemm_split_wide(uint64_t rows, uint64_t cols, uint64_t tokens) {
     return tokens > 128 || cols >= 8192 || (rows + 255) / 256 >= 64;
 }
 // The matrix-core GEMM's tiling for g.n rows, g.t tokens (both tilings have
-// an even number of 32-row groups per wave, as a swiglu launch needs). Four
-// K stages in registers ahead of the LDS stage (3 and 6 measured slower).
+// an even number of 32-row groups per wave, as a swiglu launch needs). Three
+// K stages in registers ahead of the LDS stages (2 and 4 measured within
+// 1-4 % of it, either way, with three LDS buffers).
 // The weights are read with ordinary loads: each 64-byte stage of a row is
 // half a 128-byte cache line whose other half the next stage reads, and
 // non-temporal loads, which let the line go, measured slower in place (C4 at
@@ -2012,8 +2051,8 @@ static bool gemm_split_wide(uint64_t rows, uint64_t cols, uint64_t tokens) {
 static hipError_t gemm_split_route(hipStream_t stream, const GemmSplit &g, const GemmWorkspace &ws,
                                    bool planes_ready) {
     return gemm_split_wide(g.n, g.k, g.t)
-               ? gemm_split_variant<1, 4, 2, 2, 4>(stream, g, ws, planes_ready)
-               : gemm_split_variant<1, 2, 2, 2, 4>(stream, g, ws, planes_ready);
+               ? gemm_split_variant<1, 4, 2, 2, 3>(stream, g, ws, planes_ready)
+               : gemm_split_variant<1, 2, 2, 2, 3>(stream, g, ws, planes_ready);
 }
 // Rows of one tile of the route above (the swiglu pairing needs the
 // intermediate size to be whole half tiles).
