@@ -1403,11 +1403,13 @@ static hipError_t gemm_split_variant(hipStream_t stream, GemmSplit g, const Gemm
     const uint32_t tiles = nt * mt, stages = g.k / kSplitBK;
     g.tp = mt * BM;
     if ((uint64_t)3 * g.tp * g.k > ws.plane_elems) return hipErrorInvalidValue;
-    // About one block per CU (measured against 128, 384 and 512: each K split
-    // adds a partial tile to write and sum), each split at least four stages.
+    // At most one block per CU (each K split adds a partial tile to write and
+    // sum; C4 at 443 tokens, O: 4 splits 61 us, 2 splits 55; QKV: 2 splits
+    // 95, 1 split 93; at 116 tokens QKV with 2 splits ties 4), each split at
+    // least four stages.
     uint32_t splits = 1;
-    while (tiles * splits < 256 && stages % (2 * splits) == 0 && stages / (2 * splits) >= 4 &&
-           splits < 8)
+    while (tiles * splits * 2 <= 256 && stages % (2 * splits) == 0 &&
+           stages / (2 * splits) >= 4 && splits < 8)
         splits *= 2;
     // Fewer splits while the partial tiles exceed the workspace (not straight
     // to one: a 96-tile projection would then leave most CUs idle).
