@@ -56,15 +56,23 @@ def capture(inst: plamo_hip.Instance, rows: int):
 
 
 def restore(inst: plamo_hip.Instance, snap, rows: int):
-    """runtime/engine.c:46-55 request reset, then runtime/prompt_cache.c:62-82."""
+    """runtime/engine.c:46-55 request reset, then runtime/prompt_cache.c:62-82.
+    The arrays' numpy views are made once per instance (they never move), so
+    the timed restore is the copies and counter stores the C engine makes,
+    without the cost of building 3 x layers ctypes views per call."""
+    views = getattr(inst, "_restore_views", None)
+    if views is None:
+        views = [(inst.kv(i, "k"), inst.kv(i, "v"), inst.kv(i, "rot"), inst.cache(i),
+                  inst.rotation(i)) for i in range(inst.model.count)]
+        inst._restore_views = views
     inst.reset()
-    for i, (k, v, rot, scale) in enumerate(snap):
-        inst.kv(i, "k")[:rows] = k
-        inst.kv(i, "v")[:rows] = v
-        inst.kv(i, "rot")[:rows] = rot
-        inst.cache(i).count = rows
-        inst.rotation(i).processed_count = rows
-        inst.rotation(i).scale_bits = scale
+    for (k, v, rot, scale), (vk, vv, vr, cache, rotation) in zip(snap, views):
+        vk[:rows] = k
+        vv[:rows] = v
+        vr[:rows] = rot
+        cache.count = rows
+        rotation.processed_count = rows
+        rotation.scale_bits = scale
 
 
 def prefill_flop_parts(cfg: dict, prefix: int, tokens: int) -> tuple[float, float]:

@@ -101,6 +101,11 @@ struct plamo_metal {
     // are final), overlapping the later layers.
     hipStream_t copy_stream = nullptr;
     hipEvent_t layer_events[kMaxLayers] = {};
+    // A prompt's restored-prefix upload runs on copy_stream, beside the
+    // prompt's first launches; upload_event marks its end, and the first
+    // launch that reads cached rows waits for it (upload_pending).
+    hipEvent_t upload_event = nullptr;
+    bool upload_pending = false;
     std::vector<Range> ranges;
     bool hooks = false;
 
@@ -440,6 +445,8 @@ int ensure_kv_rows(plamo_metal *m, Layer &l, uint64_t rows) {
           *rot = dev_alloc<float>(m, target * l.width);
     if (!k || !v || !rot) return 0;
     if (l.rows) {
+        // A pending prefix upload may still be writing the old rows.
+        if (m->upload_pending) HIP_TRY(m, hipStreamWaitEvent(m->stream, m->upload_event, 0));
         uint64_t bytes = l.rows * l.width * 4;
         HIP_TRY(m, hipMemcpyAsync(k, l.k, bytes, hipMemcpyDeviceToDevice, m->stream));
         HIP_TRY(m, hipMemcpyAsync(v, l.v, bytes, hipMemcpyDeviceToDevice, m->stream));
@@ -771,7 +778,20 @@ int sync_from_host(plamo_metal *m, struct model *model, std::vector<char> &stale
         d.synced = false;
     }
     // The kernel reads the table on the stream; the previous call's upload has
-    // completed, since every call waits for its work.
+    // completed, since every call waits for its work. At prompt entry it runs
+    // on copy_stream, after whatever the stream holds (reallocation copies of
+    // the same rows), while the prompt's embedding, norm and first
+    // projection need no cached row (C4 128-token prompt: the 4.7 MB of a
+    // restored 12-token prefix cross the bus in ~80 us).
+    m->upload_pending = false;
+    if (prompt_entry && entries) {
+        HIP_TRY(m, hipEventRecord(m->upload_event, m->stream));
+        HIP_TRY(m, hipStreamWaitEvent(m->copy_stream, m->upload_event, 0));
+        HIP_TRY(m, launch_copy_rows(m->copy_stream, m->upload_view, entries));
+        HIP_TRY(m, hipEventRecord(m->upload_event, m->copy_stream));
+        m->upload_pending = true;
+        return 1;
+    }
     HIP_TRY(m, launch_copy_rows(m->stream, m->upload_view, entries));
     return 1;
 }
@@ -1147,7 +1167,7 @@ struct plamo_metal *plamo_metal_open(const struct plamo_metal_config *config, ch
     snprintf(m->info.precision, sizeof m->info.precision, "fp32");
     snprintf(m->info.weight_storage, sizeof m->info.weight_storage, "hbm-bf16");
     m->info.recommended_working_set_bytes = prop.totalGlobalMem;
-    bool events = true;
+    bool events = hipEventCreateWithFlags(&m->upload_event, hipEventDisableTiming) == hipSuccess;
     for (hipEvent_t &e : m->layer_events)
         events = events && hipEventCreateWithFlags(&e, hipEventDisableTiming) == hipSuccess;
     if (!events || hipStreamCreateWithFlags(&m->stream, hipStreamNonBlocking) != hipSuccess ||
@@ -1228,6 +1248,7 @@ void plamo_metal_close(struct plamo_metal *m) {
     if (m->copy_stream) (void)hipStreamDestroy(m->copy_stream);
     for (hipEvent_t e : m->layer_events)
         if (e) (void)hipEventDestroy(e);
+    if (m->upload_event) (void)hipEventDestroy(m->upload_event);
     delete m;
 }
 
@@ -1468,6 +1489,10 @@ int run_prompt(plamo_metal *m, struct model *model, const uint32_t *ids, uint64_
         HIP_FAIL(m, launch_gemm(s, norm, h, d.qkv, qkv_w, h, T, qkv, qkv_w, ws, qkv_planes));
         qkv_planes = false;
         ++n;
+        if (m->upload_pending) {  // cached rows are read from here on
+            HIP_FAIL(m, hipStreamWaitEvent(s, m->upload_event, 0));
+            m->upload_pending = false;
+        }
         if (stale[i] && (verify || !overflow[i])) {
             HIP_FAIL(m, launch_rerotate(s, d.k, d.rot, rope.table, c->count, d.kh, d.dim));
             d.verify_stale = verify;
