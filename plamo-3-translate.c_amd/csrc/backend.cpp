@@ -765,6 +765,12 @@ int sync_from_host(plamo_metal *m, struct model *model, std::vector<char> &stale
         const bool rotated = r->processed_count == c->count && r->scale_bits == scale;
         const bool viewed = m->host_direct && d.host_k && d.host_v && d.host_rot;
         if (bytes && viewed) {
+            // A call that returned early may have left its upload running:
+            // it reads this table until it finishes.
+            if (!entries) {
+                HIP_TRY(m, hipStreamSynchronize(m->copy_stream));
+                HIP_TRY(m, hipStreamSynchronize(m->stream));
+            }
             m->upload_table[entries++] = CopyRow{d.host_k, d.k, floats};
             m->upload_table[entries++] = CopyRow{d.host_v, d.v, floats};
             if (rotated) m->upload_table[entries++] = CopyRow{d.host_rot, d.rot, floats};
