@@ -1260,10 +1260,9 @@ __global__ __launch_bounds__(64 * GM * GN, (WN > 2 || GM * GN > 4) ? 1 : 2) void
     // MFMAs, writes stage j + 2 into the third buffer, and the next step
     // starts on its MFMAs right after the one barrier per step. Stage s
     // lives in register slot s % PD from its load (step s - 2 - PD) to its
-    // LDS write (step s - 2). Loads past the last stage are clamped to it, so
-    // every step issues the same loads and the compiler keeps exact wait
-    // counts; writes past the last stage land in a buffer no step reads.
-    // Every split has at least two stages (K is a multiple of 64).
+    // LDS write (step s - 2). Loads past the last stage are clamped to it and
+    // writes past the last stage land in a buffer no step reads. Every split
+    // has at least two stages (K is a multiple of 64).
 #pragma unroll
     for (int sl = 0; sl < PD; ++sl) load(sl, sl);
     store(0, 0);
@@ -1275,47 +1274,57 @@ __global__ __launch_bounds__(64 * GM * GN, (WN > 2 || GM * GN > 4) ? 1 : 2) void
     bf16x8 a0[3][WM], b0[WN], a1[3][WM], b1[WN];
     frag(0, 0, a0, b0);
     uint32_t cur = 0;  // LDS buffer of stage j
-    for (uint32_t j0 = 0; j0 < nst; j0 += PD) {
+    auto step = [&](int sl, uint32_t j) {
+        const int ps = (sl + 2) % PD;  // register slot of stage j + 2
+        const uint32_t nxt = cur == 2 ? 0 : cur + 1, nn = nxt == 2 ? 0 : nxt + 1;
+        frag(cur, 1, a1, b1);
+        mfma(a0, b0);
+        store(ps, nn);
+        load(ps, j + 2 + PD);
+        frag(nxt, 0, a0, b0);
+        mfma(a1, b1);
+        // Issue order: per MFMA one second-step read, then one LDS write with
+        // one global load, then one next-stage read; the matrix cores never
+        // wait behind the barrier for LDS (C4 prefill GEMMs 7-12 % faster
+        // than reads after the barrier and writes after the MFMAs).
 #pragma unroll
-        for (int sl = 0; sl < PD; ++sl) {
-            const uint32_t j = j0 + sl;
-            const int ps = (sl + 2) % PD;  // register slot of stage j + 2
-            const uint32_t nxt = cur == 2 ? 0 : cur + 1, nn = nxt == 2 ? 0 : nxt + 1;
-            if (j < nst) {
-                frag(cur, 1, a1, b1);
-                mfma(a0, b0);
-                store(ps, nn);
-                load(ps, j + 2 + PD);
-                frag(nxt, 0, a0, b0);
-                mfma(a1, b1);
-                // Issue order: per MFMA one second-step read, then one LDS
-                // write with one global load, then one next-stage read; the
-                // matrix cores never wait behind the barrier for LDS (C4
-                // prefill GEMMs 7-12 % faster than reads after the barrier and
-                // writes after the MFMAs).
-#pragma unroll
-                for (int i = 0; i < NF; ++i) {
-                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // LDS read
-                }
-#pragma unroll
-                for (int i = 0; i < APT + WPT; ++i) {
-                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                    __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);  // LDS write
-                    __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // global load
-                }
-#pragma unroll
-                for (int i = 0; i < NF; ++i) {
-                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-                }
-                if constexpr (2 * NMF > 2 * NF + APT + WPT)
-                    __builtin_amdgcn_sched_group_barrier(0x008, 2 * NMF - 2 * NF - APT - WPT, 0);
-            }
-            __syncthreads();
-            cur = nxt;
+        for (int i = 0; i < NF; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // LDS read
         }
+#pragma unroll
+        for (int i = 0; i < APT + WPT; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);  // LDS write
+            __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // global load
+        }
+#pragma unroll
+        for (int i = 0; i < NF; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        }
+        if constexpr (2 * NMF > 2 * NF + APT + WPT)
+            __builtin_amdgcn_sched_group_barrier(0x008, 2 * NMF - 2 * NF - APT - WPT, 0);
+        // Each step is its own issue-order region, its MFMAs ahead of the
+        // barrier.
+        __builtin_amdgcn_sched_barrier(0);
+        __syncthreads();
+        __builtin_amdgcn_sched_barrier(0);
+        cur = nxt;
+    };
+    // Whole rounds of PD steps run without a branch, so every path into a
+    // step has issued the same loads and the compiler's wait before each LDS
+    // write lets the PD - 1 younger stages' loads stay in flight (a skipped
+    // step on some path would make it wait for nearly all of them). The last
+    // nst % PD steps follow.
+    uint32_t j0 = 0;
+    for (; j0 + PD <= nst; j0 += PD) {
+#pragma unroll
+        for (int sl = 0; sl < PD; ++sl) step(sl, j0 + sl);
     }
+#pragma unroll
+    for (int sl = 0; sl + 1 < PD; ++sl)
+        if (j0 + sl < nst) step(sl, j0 + sl);
 
     // D layout of v_mfma_f32_32x32x16: value v of lane l is row
     // 8 (v / 4) + 4 (l / 32) + v % 4, column l % 32 of the 32 x 32 tile.
