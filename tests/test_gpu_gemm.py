@@ -70,6 +70,39 @@ def test_split_bf16_gemm(oracle, tokens):
         s.close()
 
 
+@pytest.mark.parametrize("hidden", [192, 320])
+def test_split_bf16_gemm_stage_counts(oracle, hidden):
+    # The matrix-core GEMM runs its 32-column K stages in unrolled rounds of
+    # three steps and the last K % 96 / 32 steps after them: hidden 192 is
+    # six stages (two whole rounds), 320 is ten (three rounds and one more);
+    # down (K 512, split in four) has four stages per split.
+    s = plamo_hip.Synthetic(hidden, 1, hidden // 64, 1, 64, 512, 300, window=4,
+                            global_capacity=64, pattern=1, seed=12)
+    a = s.instance()
+    be = plamo_hip.Backend(s)
+    try:
+        mlp = a.layer(0).mlp.contents
+        cases = [("gate_up", mlp.gu, 1024, hidden), ("head", a.model.head, 300, hidden),
+                 ("down", mlp.down, hidden, 512)]
+        rng = np.random.default_rng(hidden)
+        for tokens in (40, 130):
+            for name, ptr, rows, cols in cases:
+                say(f"gemm stages {name} hidden={hidden} tokens={tokens}")
+                x = rng.standard_normal((tokens, cols)).astype(np.float32)
+                r, y = be.linear(ptr, x, rows)
+                assert r == 1
+                gate(y, reference(oracle, ptr, x, rows), f"{name} hidden={hidden} tokens={tokens}")
+                exact = x.astype(np.float64) @ weights_f64(ptr, rows, cols).T
+                err = np.sqrt(np.sum((y - exact) ** 2) / np.sum(exact ** 2))
+                assert err <= 3e-6, f"{name}: relative L2 {err:.3g} against the float64 product"
+        info = be.info()
+        assert info.errors == 0 and info.cpu_fallbacks == 0
+    finally:
+        be.close()
+        a.close()
+        s.close()
+
+
 @pytest.mark.parametrize("tokens", [1, 3, 5, 8, 13, 16])
 def test_skinny_gemm_two_row_tiles(oracle, tokens):
     # gate/up of MLP 8200 is N=16400 (two 16-row tiles per block, the last
