@@ -126,8 +126,9 @@ def host_threads() -> tuple[int, int]:
 
 
 def smaller_config_baseline(lib, name: str, threads: int) -> dict:
-    """C2 / C3 on the C oracle (decode s/step and the
-    128-token prefill, at N threads and at 1 thread). The whole 128-token
+    """C2 / C3 on the C oracle: decode s/step and the 128-token prefill, at N
+    threads and at 1 thread, rows split over threads as
+    runtime/parallel.c:35-48. The whole 128-token
     prompt is prefilled at N threads; at 1 thread its first two layers are,
     scaled by the layer count. Decode steps follow the prompt greedily: three
     at N threads, one at 1 thread."""
@@ -173,7 +174,7 @@ def smaller_config_baseline(lib, name: str, threads: int) -> dict:
 
 def cpu_baseline(inst: plamo_hip.Instance, token: int, seconds: float, cfg: dict, prompt,
                  snap) -> dict:
-    """The C oracle on the host cores, on bounded
+    """The C oracle on the host cores (rows split as runtime/parallel.c:35-48), on bounded
     samples of the same workloads: decode steps of the model continuing the
     GPU's sequence on the same host arrays at N threads and at 1 thread, the
     C1 layer step at both, and the 128-token prompt's prefill
