@@ -62,3 +62,16 @@ def test_config_reader_under_sanitizers(tmp_path):
     assert r.returncode == 0, r.stdout + r.stderr[-4000:]
     assert r.stdout.startswith("done 4000 iterations")
     assert (tmp_path / "ck" / "config.json").read_bytes() == before
+
+
+@needs_gcc
+def test_host_lifecycle_under_sanitizers(tmp_path):
+    # Synthetic build, page-locked instances, the prefix capture/restore copies
+    # and the per-layer host-mirror rows of 69-, 116- and 443-token prompts
+    # (sliding layers overflowing), release and free, with the arrays' page
+    # tails poisoned past each cache's capacity.
+    exe = build(tmp_path, "lifecycle_asan.c")
+    r = subprocess.run([str(exe), "3"], capture_output=True, text=True, timeout=600,
+                       env=dict(os.environ, ASAN_OPTIONS="detect_leaks=1"))
+    assert r.returncode == 0, r.stdout + r.stderr[-4000:]
+    assert r.stdout.startswith("done 3 cycles")
