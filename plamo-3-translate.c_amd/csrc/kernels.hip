@@ -2059,8 +2059,20 @@ static bool gemm_split_wide(uint64_t rows, uint64_t cols, uint64_t tokens) {
 // 443 tokens: QKV 114.1 -> 97.2 us, O 67.9 -> 60.6, gate/up 381.9 -> 362.5,
 // down 200.0 -> 187.5; at 116: QKV 40.6 -> 36.9, gate/up equal within the
 // spread between boxes).
+// Past 128 tokens, a projection whose 256-row tiles leave CUs idle takes
+// 192-row tiles when their count still fits one round of 256 blocks (not for
+// SwiGLU, whose gate/up pairing needs an even number of 32-row groups per
+// wave): C4 QKV at 443 tokens, 7 x 24 = 168 against 7 x 32 = 224 blocks,
+// 87.4-89.3 -> 81.7-85.7 us with planes ready.
+static bool gemm_split_192(const GemmSplit &g) {
+    if (g.swiglu || g.t <= 128 || g.n % 192) return false;
+    const uint64_t mt = (g.t + kSplitBM - 1) / kSplitBM;
+    const uint64_t b256 = mt * ((g.n + 255) / 256), b192 = mt * (g.n / 192);
+    return b256 < 256 && b192 <= 256 && b192 > b256;
+}
 static hipError_t gemm_split_route(hipStream_t stream, const GemmSplit &g, const GemmWorkspace &ws,
                                    bool planes_ready) {
+    if (gemm_split_192(g)) return gemm_split_variant<1, 3, 2, 2, 3>(stream, g, ws, planes_ready);
     return gemm_split_wide(g.n, g.k, g.t)
                ? gemm_split_variant<1, 4, 2, 2, 3>(stream, g, ws, planes_ready)
                : gemm_split_variant<1, 2, 2, 2, 3>(stream, g, ws, planes_ready);
