@@ -103,6 +103,33 @@ def test_split_bf16_gemm_stage_counts(oracle, hidden):
         s.close()
 
 
+@pytest.mark.parametrize("tokens", [130, 200])
+def test_split_bf16_gemm_192_row_tiles(oracle, tokens):
+    # Past 128 tokens a projection whose 256-row tiles leave CUs idle takes
+    # 192-row tiles: gate/up of MLP 768 as a plain linear is 1536 rows, 6
+    # tiles of 256 or 8 of 192 per 64 tokens.
+    s = plamo_hip.Synthetic(256, 1, 2, 1, 128, 768, 300, window=4, global_capacity=64,
+                            pattern=1, seed=13)
+    a = s.instance()
+    be = plamo_hip.Backend(s)
+    try:
+        ptr, rows, cols = a.layer(0).mlp.contents.gu, 1536, 256
+        say(f"gemm 192-row tiles tokens={tokens}")
+        x = np.random.default_rng(tokens).standard_normal((tokens, cols)).astype(np.float32)
+        r, y = be.linear(ptr, x, rows)
+        assert r == 1
+        gate(y, reference(oracle, ptr, x, rows), f"192-row tiles tokens={tokens}")
+        exact = x.astype(np.float64) @ weights_f64(ptr, rows, cols).T
+        err = np.sqrt(np.sum((y - exact) ** 2) / np.sum(exact ** 2))
+        assert err <= 3e-6, f"relative L2 {err:.3g} against the float64 product"
+        info = be.info()
+        assert info.errors == 0 and info.cpu_fallbacks == 0
+    finally:
+        be.close()
+        a.close()
+        s.close()
+
+
 @pytest.mark.parametrize("tokens", [1, 3, 5, 8, 13, 16])
 def test_skinny_gemm_two_row_tiles(oracle, tokens):
     # gate/up of MLP 8200 is N=16400 (two 16-row tiles per block, the last
